@@ -1,0 +1,113 @@
+/* C ABI of the MI355X paged INT8-KV split-K decode-attention library
+ * (libkvbridge_amd.so).  Plain C types only: device buffers are raw pointers,
+ * the HIP stream is passed as void* (a hipStream_t, NULL = default stream).
+ *
+ * Every kvb_* entry point below replaces one function of the reference C++
+ * API (cited per declaration) or is an additive extension (marked).  Calls
+ * return KVB_OK or an error code; kvb_last_error() then holds the message of
+ * the exception the reference would have thrown.  KVB_EINVAL corresponds to
+ * std::invalid_argument (raised before anything is enqueued), KVB_ERUNTIME
+ * to std::runtime_error (a HIP launch or setup failure).  Kernel execution is
+ * asynchronous: device-side faults surface at the caller's synchronization.
+ * The library allocates nothing; all buffers and the stream belong to the
+ * caller.  No global state except the thread-local error message. */
+#ifndef KVBRIDGE_C_H
+#define KVBRIDGE_C_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { KVB_OK = 0, KVB_EINVAL = 1, KVB_ERUNTIME = 2 };
+enum { KVB_OUT_NONE = 0, KVB_OUT_F32 = 1, KVB_OUT_F16 = 2 };
+enum { KVB_KERNEL_TILED_MFMA = 1, KVB_KERNEL_GENERIC = 2 };
+
+/* Mirrors kvbridge::Shape (reference include/kvbridge/attention_shape.h:9-13);
+ * the bool becomes a uint32_t so the struct has one C layout. */
+typedef struct kvb_shape {
+  uint32_t rows, q_heads, kv_heads, dim, page_tokens, pages, tokens, begin, end;
+  float scale;
+  uint32_t int8;
+} kvb_shape;
+
+/* Mirrors kvbridge::DeviceInput (reference include/kvbridge/attention_common.h:54-63). */
+typedef struct kvb_device_input {
+  const float* q;
+  const int64_t* q_positions;
+  const int64_t* k_positions;
+  const uint32_t* page_table;
+  const void* k;
+  const void* v;
+  const float* k_scales;
+  const float* v_scales;
+} kvb_device_input;
+
+/* Message of the last failed kvb_* call on this thread ("" if none). */
+const char* kvb_last_error(void);
+
+/* kvbridge::kSplitTokens (reference attention_shape.h:7). */
+uint32_t kvb_split_tokens(void);
+
+/* kvbridge::attention_shape_error (reference src/attention_shape.cpp:20-46):
+ * NULL when valid, else the first failed rule's message. */
+const char* kvb_shape_error(const kvb_shape* s);
+/* kvbridge::attention_shape_valid (reference src/attention_shape.cpp:48). */
+int kvb_shape_valid(const kvb_shape* s);
+/* kvbridge::split_count (reference src/attention_shape.cpp:52-55). */
+int kvb_split_count(const kvb_shape* s, uint32_t* splits);
+/* kvbridge::scratch_elements (reference src/attention_shape.cpp:56-59). */
+int kvb_scratch_elements(const kvb_shape* s, size_t* elements);
+/* kvbridge::output_scalar_elements (reference src/attention_shape.cpp:60-63). */
+int kvb_output_scalar_elements(const kvb_shape* s, size_t* elements);
+/* kvbridge::output_numerator_elements (reference src/attention_shape.cpp:64-66). */
+int kvb_output_numerator_elements(const kvb_shape* s, size_t* elements);
+/* kvbridge::attention_mma_supported (reference src/attention_shape.cpp:67-70). */
+int kvb_mma_supported(const kvb_shape* s);
+
+/* kvbridge::preload_attention_kernels / _reference_kernels / _mma_kernels
+ * (reference include/kvbridge/attention_common.h:69-72, src/attention_shared.cu:376-387,
+ * src/attention_mma.cu:13-31).  Return a hipError_t value (0 = success). */
+int kvb_preload_attention_kernels(void);
+int kvb_preload_attention_reference_kernels(void);
+int kvb_preload_attention_mma_kernels(void);
+
+/* kvbridge::launch_attention (reference include/kvbridge/attention_common.h:80-81,
+ * src/attention_shared.cu:339-366): kSplitTokens-token split partials + merge. */
+int kvb_launch_attention(const kvb_shape* s, const kvb_device_input* in, float* scratch,
+                         float* m, float* l, float* n, void* stream);
+/* kvbridge::launch_attention_mma (reference include/kvbridge/attention_common.h:90-91,
+ * src/attention_mma.cu:33-45): same outputs; KVB_EINVAL unless kvb_mma_supported. */
+int kvb_launch_attention_mma(const kvb_shape* s, const kvb_device_input* in, float* scratch,
+                             float* m, float* l, float* n, void* stream);
+/* kvbridge::merge_attention (reference include/kvbridge/attention_common.h:95-96,
+ * src/attention_shared.cu:368-374): splits must equal kvb_split_count. */
+int kvb_merge_attention(const kvb_shape* s, const float* scratch, uint32_t splits,
+                        float* m, float* l, float* n, void* stream);
+
+/* Extension: split count / scratch size for caller-chosen split_tokens. */
+int kvb_split_count_ex(const kvb_shape* s, uint32_t split_tokens, uint32_t* splits);
+int kvb_scratch_elements_ex(const kvb_shape* s, uint32_t split_tokens, size_t* elements);
+/* Extension: split partials only, split_tokens tokens per split. */
+int kvb_split_attention(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens,
+                        float* scratch, void* stream);
+/* Extension: LSE merge of `splits` partials, plus the normalized output
+ * out[rh*dim+d] = l > 0 ? n/l : 0 in out_type (KVB_OUT_F32 / KVB_OUT_F16),
+ * or no output for KVB_OUT_NONE (out may then be NULL). */
+int kvb_merge_finalize(const kvb_shape* s, const float* scratch, uint32_t splits,
+                       float* m, float* l, float* n, void* out, int out_type, void* stream);
+/* Extension: kvb_split_attention then kvb_merge_finalize on one stream. */
+int kvb_decode_attention(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens,
+                         float* scratch, float* m, float* l, float* n, void* out, int out_type,
+                         void* stream);
+/* Extension (diagnostic): which split kernel kvb_split_attention would run for
+ * these arguments: KVB_KERNEL_TILED_MFMA or KVB_KERNEL_GENERIC; 0 if invalid. */
+int kvb_selected_kernel(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVBRIDGE_C_H */

@@ -1,0 +1,79 @@
+// C++ API (include/kvbridge/attention_common.h, attention_ext.h) as a thin
+// layer over the extern "C" entry points.  Status codes become the
+// reference's exception types: KVB_EINVAL -> std::invalid_argument,
+// KVB_ERUNTIME -> std::runtime_error (reference src/attention_launch_checks.h:8-27).
+#include <stdexcept>
+
+#include "kvbridge/attention_ext.h"
+#include "kvbridge_c.h"
+
+namespace kvbridge {
+namespace {
+
+kvb_shape c_shape(const Shape& s) {
+  return kvb_shape{s.rows, s.q_heads, s.kv_heads, s.dim, s.page_tokens, s.pages,
+                   s.tokens, s.begin, s.end, s.scale, s.int8 ? 1u : 0u};
+}
+
+kvb_device_input c_input(const DeviceInput& in) {
+  return kvb_device_input{in.q, in.q_positions, in.k_positions, in.page_table,
+                          in.k, in.v, in.k_scales, in.v_scales};
+}
+
+void check(int rc) {
+  if (rc == KVB_OK) return;
+  if (rc == KVB_EINVAL) throw std::invalid_argument(kvb_last_error());
+  throw std::runtime_error(kvb_last_error());
+}
+
+}  // namespace
+
+hipError_t preload_attention_kernels() { return hipError_t(kvb_preload_attention_kernels()); }
+hipError_t preload_attention_reference_kernels() {
+  return hipError_t(kvb_preload_attention_reference_kernels());
+}
+hipError_t preload_attention_mma_kernels() { return hipError_t(kvb_preload_attention_mma_kernels()); }
+
+void launch_attention(const Shape& s, const DeviceInput& in, float* scratch, float* m, float* l,
+                      float* n, hipStream_t stream) {
+  const kvb_shape cs = c_shape(s);
+  const kvb_device_input ci = c_input(in);
+  check(kvb_launch_attention(&cs, &ci, scratch, m, l, n, stream));
+}
+
+void launch_attention_mma(const Shape& s, const DeviceInput& in, float* scratch, float* m,
+                          float* l, float* n, hipStream_t stream) {
+  const kvb_shape cs = c_shape(s);
+  const kvb_device_input ci = c_input(in);
+  check(kvb_launch_attention_mma(&cs, &ci, scratch, m, l, n, stream));
+}
+
+void merge_attention(const Shape& s, const float* scratch, unsigned splits, float* m, float* l,
+                     float* n, hipStream_t stream) {
+  const kvb_shape cs = c_shape(s);
+  check(kvb_merge_attention(&cs, scratch, splits, m, l, n, stream));
+}
+
+void launch_split_attention(const Shape& s, const DeviceInput& in, unsigned split_tokens,
+                            float* scratch, hipStream_t stream) {
+  const kvb_shape cs = c_shape(s);
+  const kvb_device_input ci = c_input(in);
+  check(kvb_split_attention(&cs, &ci, split_tokens, scratch, stream));
+}
+
+void merge_finalize_attention(const Shape& s, const float* scratch, unsigned splits, float* m,
+                              float* l, float* n, void* out, OutputType out_type,
+                              hipStream_t stream) {
+  const kvb_shape cs = c_shape(s);
+  check(kvb_merge_finalize(&cs, scratch, splits, m, l, n, out, int(out_type), stream));
+}
+
+void decode_attention(const Shape& s, const DeviceInput& in, unsigned split_tokens,
+                      float* scratch, float* m, float* l, float* n, void* out,
+                      OutputType out_type, hipStream_t stream) {
+  const kvb_shape cs = c_shape(s);
+  const kvb_device_input ci = c_input(in);
+  check(kvb_decode_attention(&cs, &ci, split_tokens, scratch, m, l, n, out, int(out_type), stream));
+}
+
+}  // namespace kvbridge

@@ -1,0 +1,334 @@
+// extern "C" boundary (include/kvbridge_c.h): validation, kernel selection
+// and launches.  Errors never cross the C ABI as exceptions: each entry point
+// returns a status code and leaves the message in a thread-local string.
+//
+// Validation order and messages follow the reference:
+//   validate_outputs / validate_launch  src/attention_launch_checks.h:8-23
+//   split-count check of merge          src/attention_shared.cu:371
+//   MMA geometry gate                   src/attention_mma.cu:36-38
+//   launch error mapping (check_cuda)   src/attention_launch_checks.h:24-27
+#include "kvbridge_c.h"
+
+#include <hip/hip_runtime.h>
+
+#include <stdexcept>
+#include <string>
+
+#include "kernels.h"
+#include "kvbridge/attention_ext.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* msg) {
+  g_error = msg;
+  return code;
+}
+
+kvbridge::Shape to_shape(const kvb_shape& s) {
+  return kvbridge::Shape{s.rows, s.q_heads, s.kv_heads, s.dim, s.page_tokens, s.pages,
+                         s.tokens, s.begin, s.end, s.scale, s.int8 != 0};
+}
+
+kvbridge::DeviceInput to_input(const kvb_device_input& in) {
+  return kvbridge::DeviceInput{in.q, in.q_positions, in.k_positions, in.page_table,
+                               in.k, in.v, in.k_scales, in.v_scales};
+}
+
+// Returns nullptr when the outputs are acceptable, else the reference message.
+const char* outputs_error(const kvbridge::Shape& s, const void* scratch, const void* m,
+                          const void* l, const void* n) {
+  if (const char* e = kvbridge::attention_shape_error(s)) return e;
+  if (!scratch || !m || !l || !n) return "scratch, m, l and n must be non-null device buffers";
+  return nullptr;
+}
+
+const char* launch_error(const kvbridge::Shape& s, const kvbridge::DeviceInput& in,
+                         const void* scratch) {
+  if (const char* e = kvbridge::attention_shape_error(s)) return e;
+  if (!scratch) return "scratch, m, l and n must be non-null device buffers";
+  if (!in.q || !in.q_positions || !in.k_positions || !in.page_table || !in.k || !in.v ||
+      (s.int8 && (!in.k_scales || !in.v_scales)))
+    return "attention input device buffers must be non-null";
+  if (s.int8 && s.dim % 4 == 0 && s.page_tokens % 4 == 0 &&
+      ((reinterpret_cast<uintptr_t>(in.k) % 4) || (reinterpret_cast<uintptr_t>(in.v) % 4)))
+    return "vectorized INT8 K/V buffers must be 4-byte aligned";
+  return nullptr;
+}
+
+int hip_status(hipError_t e, const char* op) {
+  if (e == hipSuccess) return KVB_OK;
+  g_error = std::string(op) + ": " + hipGetErrorString(e);
+  return KVB_ERUNTIME;
+}
+
+// Split partials for a validated shape with `splits` splits of split_tokens.
+int run_split(const kvbridge::Shape& s, const kvbridge::DeviceInput& in, unsigned split_tokens,
+              unsigned splits, float* scratch, hipStream_t stream, const char* op) {
+  const kvb::SplitArgs a = kvb::make_split_args(s, in, split_tokens, splits, scratch);
+  const hipError_t e = kvb::tiled_supported(s, in) ? kvb::launch_split_tiled(a, stream)
+                                                   : kvb::launch_split_generic(a, s.int8, stream);
+  return hip_status(e, op);
+}
+
+int run_merge(const kvbridge::Shape& s, const float* scratch, unsigned splits, float* m,
+              float* l, float* n, void* out, int out_type, hipStream_t stream, const char* op) {
+  const hipError_t e = kvb::launch_merge(s.rows * s.q_heads, s.dim, splits, scratch, m, l, n,
+                                         out, out_type, stream);
+  return hip_status(e, op);
+}
+
+template <class F>
+int guarded(F&& f) {
+  try {
+    return f();
+  } catch (const std::invalid_argument& e) {
+    return fail(KVB_EINVAL, e.what());
+  } catch (const std::exception& e) {
+    return fail(KVB_ERUNTIME, e.what());
+  } catch (...) {
+    return fail(KVB_ERUNTIME, "unknown error");
+  }
+}
+
+}  // namespace
+
+namespace kvb {
+
+SplitArgs make_split_args(const kvbridge::Shape& s, const kvbridge::DeviceInput& in,
+                          unsigned split_tokens, unsigned splits, float* scratch) {
+  SplitArgs a{};
+  a.q = in.q;
+  a.q_positions = in.q_positions;
+  a.k_positions = in.k_positions;
+  a.page_table = in.page_table;
+  a.k = in.k;
+  a.v = in.v;
+  a.k_scales = in.k_scales;
+  a.v_scales = in.v_scales;
+  a.scratch = scratch;
+  a.rows = s.rows;
+  a.q_heads = s.q_heads;
+  a.kv_heads = s.kv_heads;
+  a.group = s.q_heads / s.kv_heads;
+  a.dim = s.dim;
+  a.page_tokens = s.page_tokens;
+  a.pages = s.pages;
+  a.begin = s.begin;
+  a.end = s.end;
+  a.split_tokens = split_tokens;
+  a.splits = splits;
+  a.scale = s.scale;
+  return a;
+}
+
+bool tiled_supported(const kvbridge::Shape& s, const kvbridge::DeviceInput& in) {
+  if (!s.int8) return false;
+  if (s.dim != 64 && s.dim != 128 && s.dim != 256) return false;
+  if (s.page_tokens % 16 != 0) return false;
+  const uint64_t head_rows = uint64_t(s.rows) * (s.q_heads / s.kv_heads);
+  if (uint64_t(s.kv_heads) * ((head_rows + 15) / 16) > 65535) return false;  // grid.y
+  const auto al = [](const void* p, uintptr_t n) { return reinterpret_cast<uintptr_t>(p) % n == 0; };
+  return al(in.k, 16) && al(in.v, 16) && al(in.q, 16) && al(in.k_scales, 4) && al(in.v_scales, 4);
+}
+
+}  // namespace kvb
+
+extern "C" {
+
+const char* kvb_last_error(void) { return g_error.c_str(); }
+
+uint32_t kvb_split_tokens(void) { return kvbridge::kSplitTokens; }
+
+const char* kvb_shape_error(const kvb_shape* s) {
+  if (!s) return "shape pointer must be non-null";
+  return kvbridge::attention_shape_error(to_shape(*s));
+}
+
+int kvb_shape_valid(const kvb_shape* s) {
+  return s && kvbridge::attention_shape_valid(to_shape(*s)) ? 1 : 0;
+}
+
+int kvb_split_count(const kvb_shape* s, uint32_t* splits) {
+  return guarded([&]() -> int {
+    if (!s || !splits) return fail(KVB_EINVAL, "null argument");
+    *splits = kvbridge::split_count(to_shape(*s));
+    return KVB_OK;
+  });
+}
+
+int kvb_scratch_elements(const kvb_shape* s, size_t* elements) {
+  return guarded([&]() -> int {
+    if (!s || !elements) return fail(KVB_EINVAL, "null argument");
+    *elements = kvbridge::scratch_elements(to_shape(*s));
+    return KVB_OK;
+  });
+}
+
+int kvb_output_scalar_elements(const kvb_shape* s, size_t* elements) {
+  return guarded([&]() -> int {
+    if (!s || !elements) return fail(KVB_EINVAL, "null argument");
+    *elements = kvbridge::output_scalar_elements(to_shape(*s));
+    return KVB_OK;
+  });
+}
+
+int kvb_output_numerator_elements(const kvb_shape* s, size_t* elements) {
+  return guarded([&]() -> int {
+    if (!s || !elements) return fail(KVB_EINVAL, "null argument");
+    *elements = kvbridge::output_numerator_elements(to_shape(*s));
+    return KVB_OK;
+  });
+}
+
+int kvb_mma_supported(const kvb_shape* s) {
+  return s && kvbridge::attention_mma_supported(to_shape(*s)) ? 1 : 0;
+}
+
+int kvb_preload_attention_reference_kernels(void) {
+  hipError_t e = kvb::preload_generic();
+  if (e == hipSuccess) e = kvb::preload_tiled();
+  if (e == hipSuccess) e = kvb::preload_merge();
+  return int(e);
+}
+
+int kvb_preload_attention_mma_kernels(void) {
+  // The dense multi-row geometry runs on the tiled MFMA kernel; any gfx950
+  // device qualifies.  Checks that a device is current and the code object
+  // holds the kernels for it.
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return int(e);
+  e = kvb::preload_tiled();
+  if (e == hipSuccess) e = kvb::preload_merge();
+  return int(e);
+}
+
+int kvb_preload_attention_kernels(void) {
+  const int e = kvb_preload_attention_reference_kernels();
+  return e != 0 ? e : kvb_preload_attention_mma_kernels();
+}
+
+int kvb_launch_attention(const kvb_shape* sp, const kvb_device_input* ip, float* scratch,
+                         float* m, float* l, float* n, void* stream) {
+  return guarded([&]() -> int {
+    if (!sp || !ip) return fail(KVB_EINVAL, "shape and input descriptors must be non-null");
+    const kvbridge::Shape s = to_shape(*sp);
+    const kvbridge::DeviceInput in = to_input(*ip);
+    if (const char* e = outputs_error(s, scratch, m, l, n)) return fail(KVB_EINVAL, e);
+    if (const char* e = launch_error(s, in, scratch)) return fail(KVB_EINVAL, e);
+    const unsigned splits = kvbridge::split_count(s);
+    const auto st = static_cast<hipStream_t>(stream);
+    int rc = run_split(s, in, kvbridge::kSplitTokens, splits, scratch, st, "split launch");
+    if (rc != KVB_OK) return rc;
+    return run_merge(s, scratch, splits, m, l, n, nullptr, KVB_OUT_NONE, st, "merge launch");
+  });
+}
+
+int kvb_launch_attention_mma(const kvb_shape* sp, const kvb_device_input* ip, float* scratch,
+                             float* m, float* l, float* n, void* stream) {
+  return guarded([&]() -> int {
+    if (!sp || !ip) return fail(KVB_EINVAL, "shape and input descriptors must be non-null");
+    const kvbridge::Shape s = to_shape(*sp);
+    const kvbridge::DeviceInput in = to_input(*ip);
+    if (const char* e = outputs_error(s, scratch, m, l, n)) return fail(KVB_EINVAL, e);
+    if (const char* e = launch_error(s, in, scratch)) return fail(KVB_EINVAL, e);
+    if (!kvbridge::attention_mma_supported(s))
+      return fail(KVB_EINVAL,
+                  "launch_attention_mma requires int8 KV, rows8/group6/dim256/page32 and a page-aligned begin");
+    // The geometry always qualifies for the tiled MFMA kernel; buffers that
+    // are 4- but not 16-byte aligned take the generic kernel (same results).
+    const unsigned splits = kvbridge::split_count(s);
+    const auto st = static_cast<hipStream_t>(stream);
+    int rc = run_split(s, in, kvbridge::kSplitTokens, splits, scratch, st, "MMA split launch");
+    if (rc != KVB_OK) return rc;
+    return run_merge(s, scratch, splits, m, l, n, nullptr, KVB_OUT_NONE, st, "attention merge launch");
+  });
+}
+
+int kvb_merge_attention(const kvb_shape* sp, const float* scratch, uint32_t splits, float* m,
+                        float* l, float* n, void* stream) {
+  return guarded([&]() -> int {
+    if (!sp) return fail(KVB_EINVAL, "shape descriptor must be non-null");
+    const kvbridge::Shape s = to_shape(*sp);
+    if (const char* e = outputs_error(s, scratch, m, l, n)) return fail(KVB_EINVAL, e);
+    if (splits != kvbridge::split_count(s))
+      return fail(KVB_EINVAL, "merge split count does not match shape");
+    return run_merge(s, scratch, splits, m, l, n, nullptr, KVB_OUT_NONE,
+                     static_cast<hipStream_t>(stream), "attention merge launch");
+  });
+}
+
+int kvb_split_count_ex(const kvb_shape* s, uint32_t split_tokens, uint32_t* splits) {
+  return guarded([&]() -> int {
+    if (!s || !splits) return fail(KVB_EINVAL, "null argument");
+    *splits = kvbridge::split_count(to_shape(*s), split_tokens);
+    return KVB_OK;
+  });
+}
+
+int kvb_scratch_elements_ex(const kvb_shape* s, uint32_t split_tokens, size_t* elements) {
+  return guarded([&]() -> int {
+    if (!s || !elements) return fail(KVB_EINVAL, "null argument");
+    *elements = kvbridge::scratch_elements(to_shape(*s), split_tokens);
+    return KVB_OK;
+  });
+}
+
+int kvb_split_attention(const kvb_shape* sp, const kvb_device_input* ip, uint32_t split_tokens,
+                        float* scratch, void* stream) {
+  return guarded([&]() -> int {
+    if (!sp || !ip) return fail(KVB_EINVAL, "shape and input descriptors must be non-null");
+    const kvbridge::Shape s = to_shape(*sp);
+    const kvbridge::DeviceInput in = to_input(*ip);
+    if (const char* e = launch_error(s, in, scratch)) return fail(KVB_EINVAL, e);
+    const unsigned splits = kvbridge::split_count(s, split_tokens);
+    return run_split(s, in, split_tokens, splits, scratch, static_cast<hipStream_t>(stream),
+                     "split launch");
+  });
+}
+
+int kvb_merge_finalize(const kvb_shape* sp, const float* scratch, uint32_t splits, float* m,
+                       float* l, float* n, void* out, int out_type, void* stream) {
+  return guarded([&]() -> int {
+    if (!sp) return fail(KVB_EINVAL, "shape descriptor must be non-null");
+    const kvbridge::Shape s = to_shape(*sp);
+    if (const char* e = outputs_error(s, scratch, m, l, n)) return fail(KVB_EINVAL, e);
+    if (splits == 0 || splits > 65535) return fail(KVB_EINVAL, "split count must be in [1,65535]");
+    if (out_type != KVB_OUT_NONE && out_type != KVB_OUT_F32 && out_type != KVB_OUT_F16)
+      return fail(KVB_EINVAL, "unknown output type");
+    if (out_type != KVB_OUT_NONE && !out) return fail(KVB_EINVAL, "output buffer must be non-null");
+    return run_merge(s, scratch, splits, m, l, n, out, out_type, static_cast<hipStream_t>(stream),
+                     "attention merge launch");
+  });
+}
+
+int kvb_decode_attention(const kvb_shape* sp, const kvb_device_input* ip, uint32_t split_tokens,
+                         float* scratch, float* m, float* l, float* n, void* out, int out_type,
+                         void* stream) {
+  return guarded([&]() -> int {
+    if (!sp || !ip) return fail(KVB_EINVAL, "shape and input descriptors must be non-null");
+    const kvbridge::Shape s = to_shape(*sp);
+    const kvbridge::DeviceInput in = to_input(*ip);
+    if (const char* e = outputs_error(s, scratch, m, l, n)) return fail(KVB_EINVAL, e);
+    if (const char* e = launch_error(s, in, scratch)) return fail(KVB_EINVAL, e);
+    if (out_type != KVB_OUT_NONE && out_type != KVB_OUT_F32 && out_type != KVB_OUT_F16)
+      return fail(KVB_EINVAL, "unknown output type");
+    if (out_type != KVB_OUT_NONE && !out) return fail(KVB_EINVAL, "output buffer must be non-null");
+    const unsigned splits = kvbridge::split_count(s, split_tokens);
+    const auto st = static_cast<hipStream_t>(stream);
+    int rc = run_split(s, in, split_tokens, splits, scratch, st, "split launch");
+    if (rc != KVB_OK) return rc;
+    return run_merge(s, scratch, splits, m, l, n, out, out_type, st, "attention merge launch");
+  });
+}
+
+int kvb_selected_kernel(const kvb_shape* sp, const kvb_device_input* ip, uint32_t split_tokens) {
+  if (!sp || !ip || split_tokens == 0) return 0;
+  const kvbridge::Shape s = to_shape(*sp);
+  if (!kvbridge::attention_shape_valid(s)) return 0;
+  return kvb::tiled_supported(s, to_input(*ip)) ? KVB_KERNEL_TILED_MFMA : KVB_KERNEL_GENERIC;
+}
+
+}  // extern "C"

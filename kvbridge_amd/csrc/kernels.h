@@ -1,0 +1,44 @@
+// Internal launcher interface between the C ABI (capi.cpp) and the HIP
+// translation units.  Shapes reaching these functions are already validated.
+#pragma once
+#include <hip/hip_runtime_api.h>
+#include <cstdint>
+#include "kvbridge/attention_common.h"
+
+namespace kvb {
+
+// Arguments common to both split kernels.  Token indices are logical; every
+// physical offset fits 32 bits (attention_shape_error rejects larger KV).
+struct SplitArgs {
+  const float* q;
+  const int64_t* q_positions;
+  const int64_t* k_positions;
+  const uint32_t* page_table;
+  const void* k;
+  const void* v;
+  const float* k_scales;
+  const float* v_scales;
+  float* scratch;
+  uint32_t rows, q_heads, kv_heads, group, dim, page_tokens, pages, begin, end;
+  uint32_t split_tokens, splits;
+  float scale;
+};
+
+SplitArgs make_split_args(const kvbridge::Shape& s, const kvbridge::DeviceInput& in,
+                          unsigned split_tokens, unsigned splits, float* scratch);
+
+// Whether the tiled MFMA split kernel covers this shape and these buffers.
+bool tiled_supported(const kvbridge::Shape& s, const kvbridge::DeviceInput& in);
+
+hipError_t launch_split_tiled(const SplitArgs& a, hipStream_t stream);
+hipError_t launch_split_generic(const SplitArgs& a, bool int8, hipStream_t stream);
+// out_type: 0 none, 1 fp32, 2 fp16 (kvbridge_c.h KVB_OUT_*).
+hipError_t launch_merge(uint32_t row_heads, uint32_t dim, uint32_t splits, const float* scratch,
+                        float* m, float* l, float* n, void* out, int out_type,
+                        hipStream_t stream);
+
+hipError_t preload_tiled();
+hipError_t preload_generic();
+hipError_t preload_merge();
+
+}  // namespace kvb

@@ -1,0 +1,272 @@
+/* TEST INFRASTRUCTURE ONLY.  CPU oracle for paged INT8-KV split-K decode
+ * attention.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library, and only as the checker or the
+ * timed CPU baseline -- never as the product path.
+ *
+ * Restates, in plain C:
+ *   oracle_fp64         examples/attention_reference.h:53-90 (scalar FP64
+ *                       direct softmax; "the CPU reference path")
+ *   oracle_split_fp32   src/attention_shared.cu:42-209 semantics (per split:
+ *                       fp32 dots with the k-scale folded into K, split max,
+ *                       expf weights, v-scale folded into the weights)
+ *   oracle_merge_fp32   src/attention_shared.cu:295-335 (LSE merge, splits
+ *                       with l <= 0 skipped)
+ *   oracle_fixture      examples/attention_reference.h:19-48 (closed-form
+ *                       patterned fixture)
+ * Pinned by tests/test_oracle.py against the reference's own known-answer
+ * tests (tests/reference_test.cpp), golden vectors produced by the
+ * reference's FP64 oracle built from source (tests/golden), and closed forms. */
+#include "attention_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+static double kv_at(const oracle_shape* s, const void* base, size_t i) {
+  if (s->int8) return (double)((const int8_t*)base)[i];
+  return (double)((const float*)base)[i];
+}
+
+/* Index of (physical page, kv head, slot) in the scale arrays; K row = this * dim. */
+static size_t slot_index(const oracle_shape* s, const uint32_t* table, uint32_t t, uint32_t kv) {
+  const size_t page = table[t / s->page_tokens];
+  return (page * s->kv_heads + kv) * s->page_tokens + t % s->page_tokens;
+}
+
+/* V element (d) of logical token t: V is dim-major inside a page. */
+static size_t v_index(const oracle_shape* s, const uint32_t* table, uint32_t t, uint32_t kv, uint32_t d) {
+  const size_t page = table[t / s->page_tokens];
+  return ((page * s->kv_heads + kv) * s->dim + d) * s->page_tokens + t % s->page_tokens;
+}
+
+typedef struct {
+  const oracle_shape* s;
+  const float *q, *ks, *vs;
+  const int64_t *qpos, *kpos;
+  const uint32_t* table;
+  const void *k, *v;
+  double* out;
+  uint8_t* visible;
+  uint32_t rh_begin, rh_end;
+} fp64_job;
+
+static void fp64_rows(const fp64_job* j) {
+  const oracle_shape* s = j->s;
+  const uint32_t group = s->q_heads / s->kv_heads;
+  const uint32_t n = s->end - s->begin;
+  double* logits = (double*)malloc(sizeof(double) * (n ? n : 1));
+  for (uint32_t rh = j->rh_begin; rh < j->rh_end; ++rh) {
+    const uint32_t r = rh / s->q_heads, h = rh % s->q_heads, kv = h / group;
+    const float* q = j->q + (size_t)rh * s->dim;
+    double* o = j->out + (size_t)rh * s->dim;
+    double mx = -INFINITY;
+    int any = 0;
+    for (uint32_t d = 0; d < s->dim; ++d) o[d] = 0.0;
+    for (uint32_t t = s->begin; t < s->end; ++t) {
+      double lg = -INFINITY;
+      if (j->kpos[t] <= j->qpos[r]) {
+        const size_t si = slot_index(s, j->table, t, kv);
+        const double ks = s->int8 ? (double)j->ks[si] : 1.0;
+        double dot = 0.0;
+        for (uint32_t d = 0; d < s->dim; ++d) dot += (double)q[d] * kv_at(s, j->k, si * s->dim + d) * ks;
+        lg = dot * (double)s->scale;
+        any = 1;
+      }
+      logits[t - s->begin] = lg;
+      if (lg > mx) mx = lg;
+    }
+    j->visible[rh] = (uint8_t)any;
+    if (!any) continue;
+    double den = 0.0;
+    for (uint32_t t = s->begin; t < s->end; ++t) {
+      const double w = exp(logits[t - s->begin] - mx);
+      if (w == 0.0) continue;
+      den += w;
+      const size_t si = slot_index(s, j->table, t, kv);
+      const double vs = s->int8 ? (double)j->vs[si] : 1.0;
+      for (uint32_t d = 0; d < s->dim; ++d) o[d] += w * kv_at(s, j->v, v_index(s, j->table, t, kv, d)) * vs;
+    }
+    for (uint32_t d = 0; d < s->dim; ++d) o[d] /= den;
+  }
+  free(logits);
+}
+
+static void* fp64_thread(void* p) {
+  fp64_rows((const fp64_job*)p);
+  return NULL;
+}
+
+void oracle_fp64(const oracle_shape* s, const float* q, const int64_t* qpos, const int64_t* kpos,
+                 const uint32_t* table, const void* k, const void* v, const float* ks,
+                 const float* vs, double* out, uint8_t* visible, int threads) {
+  const uint32_t total = s->rows * s->q_heads;
+  if (threads < 1) threads = 1;
+  if ((uint32_t)threads > total) threads = (int)total;
+  fp64_job* jobs = (fp64_job*)calloc((size_t)threads, sizeof(fp64_job));
+  pthread_t* tids = (pthread_t*)calloc((size_t)threads, sizeof(pthread_t));
+  for (int i = 0; i < threads; ++i) {
+    fp64_job j = {s, q, ks, vs, qpos, kpos, table, k, v, out, visible,
+                  (uint32_t)((uint64_t)total * i / threads), (uint32_t)((uint64_t)total * (i + 1) / threads)};
+    jobs[i] = j;
+  }
+  if (threads == 1) {
+    fp64_rows(&jobs[0]);
+  } else {
+    for (int i = 0; i < threads; ++i) pthread_create(&tids[i], NULL, fp64_thread, &jobs[i]);
+    for (int i = 0; i < threads; ++i) pthread_join(tids[i], NULL);
+  }
+  free(jobs);
+  free(tids);
+}
+
+/* ---- fp32 split-K partials + LSE merge -------------------------------- */
+
+typedef struct {
+  const oracle_shape* s;
+  const float *q, *ks, *vs;
+  const int64_t *qpos, *kpos;
+  const uint32_t* table;
+  const void *k, *v;
+  uint32_t split_tokens, splits;
+  float* scratch;
+  uint32_t unit_begin, unit_end; /* units = (row*q_heads + head) * splits + split */
+} split_job;
+
+static void split_units(const split_job* j) {
+  const oracle_shape* s = j->s;
+  const uint32_t group = s->q_heads / s->kv_heads;
+  const uint32_t stride = s->dim + 2;
+  float* w = (float*)malloc(sizeof(float) * (j->split_tokens ? j->split_tokens : 1));
+  for (uint32_t u = j->unit_begin; u < j->unit_end; ++u) {
+    const uint32_t rh = u / j->splits, split = u % j->splits;
+    const uint32_t r = rh / s->q_heads, h = rh % s->q_heads, kv = h / group;
+    const float* q = j->q + (size_t)rh * s->dim;
+    float* part = j->scratch + (size_t)u * stride;
+    const uint64_t start64 = (uint64_t)s->begin + (uint64_t)split * j->split_tokens;
+    const uint32_t start = start64 < s->end ? (uint32_t)start64 : s->end;
+    const uint32_t count = (uint64_t)s->end - start < j->split_tokens ? s->end - start : j->split_tokens;
+    float mx = -INFINITY;
+    for (uint32_t i = 0; i < count; ++i) {
+      const uint32_t t = start + i;
+      float sc = -INFINITY;
+      if (j->kpos[t] <= j->qpos[r]) {
+        const size_t si = slot_index(s, j->table, t, kv);
+        const float kscale = s->int8 ? j->ks[si] : 1.0f;
+        float dot = 0.0f;
+        for (uint32_t d = 0; d < s->dim; ++d) {
+          const float kf = s->int8 ? (float)((const int8_t*)j->k)[si * s->dim + d] * kscale
+                                   : ((const float*)j->k)[si * s->dim + d];
+          dot = fmaf(q[d], kf, dot);
+        }
+        sc = dot * s->scale;
+      }
+      w[i] = sc;
+      if (sc > mx) mx = sc;
+    }
+    float den = 0.0f;
+    for (uint32_t d = 0; d < s->dim; ++d) part[2 + d] = 0.0f;
+    for (uint32_t i = 0; i < count; ++i) {
+      const float wt = mx == -INFINITY ? 0.0f : expf(w[i] - mx);
+      den += wt;
+      if (wt == 0.0f) continue;
+      const uint32_t t = start + i;
+      const size_t si = slot_index(s, j->table, t, kv);
+      const float wsc = wt * (s->int8 ? j->vs[si] : 1.0f);
+      for (uint32_t d = 0; d < s->dim; ++d) {
+        const size_t vi = v_index(s, j->table, t, kv, d);
+        const float vf = s->int8 ? (float)((const int8_t*)j->v)[vi] : ((const float*)j->v)[vi];
+        part[2 + d] = fmaf(wsc, vf, part[2 + d]);
+      }
+    }
+    part[0] = mx;
+    part[1] = den;
+  }
+  free(w);
+}
+
+static void* split_thread(void* p) {
+  split_units((const split_job*)p);
+  return NULL;
+}
+
+void oracle_split_fp32(const oracle_shape* s, const float* q, const int64_t* qpos,
+                       const int64_t* kpos, const uint32_t* table, const void* k, const void* v,
+                       const float* ks, const float* vs, uint32_t split_tokens, uint32_t splits,
+                       float* scratch, int threads) {
+  const uint32_t total = s->rows * s->q_heads * splits;
+  if (threads < 1) threads = 1;
+  if ((uint32_t)threads > total) threads = (int)total;
+  split_job* jobs = (split_job*)calloc((size_t)threads, sizeof(split_job));
+  pthread_t* tids = (pthread_t*)calloc((size_t)threads, sizeof(pthread_t));
+  for (int i = 0; i < threads; ++i) {
+    split_job j = {s, q, ks, vs, qpos, kpos, table, k, v, split_tokens, splits, scratch,
+                   (uint32_t)((uint64_t)total * i / threads), (uint32_t)((uint64_t)total * (i + 1) / threads)};
+    jobs[i] = j;
+  }
+  if (threads == 1) {
+    split_units(&jobs[0]);
+  } else {
+    for (int i = 0; i < threads; ++i) pthread_create(&tids[i], NULL, split_thread, &jobs[i]);
+    for (int i = 0; i < threads; ++i) pthread_join(tids[i], NULL);
+  }
+  free(jobs);
+  free(tids);
+}
+
+void oracle_merge_fp32(const oracle_shape* s, const float* scratch, uint32_t splits, float* m,
+                       float* l, float* n) {
+  const uint32_t stride = s->dim + 2;
+  for (uint32_t rh = 0; rh < s->rows * s->q_heads; ++rh) {
+    const float* base = scratch + (size_t)rh * splits * stride;
+    float mx = -INFINITY;
+    for (uint32_t j = 0; j < splits; ++j)
+      if (base[(size_t)j * stride] > mx) mx = base[(size_t)j * stride];
+    float den = 0.0f;
+    for (uint32_t d = 0; d < s->dim; ++d) n[(size_t)rh * s->dim + d] = 0.0f;
+    for (uint32_t j = 0; j < splits; ++j) {
+      const float* p = base + (size_t)j * stride;
+      if (!(p[1] > 0.0f)) continue;
+      const float f = expf(p[0] - mx);
+      den += f * p[1];
+      for (uint32_t d = 0; d < s->dim; ++d)
+        n[(size_t)rh * s->dim + d] = fmaf(f, p[2 + d], n[(size_t)rh * s->dim + d]);
+    }
+    m[rh] = mx;
+    l[rh] = den;
+  }
+}
+
+/* ---- closed-form fixture ----------------------------------------------
+ * Shape {8, 24, 4, 256, 32, ceil(tokens/32), tokens, 0, tokens, 1/16, int8}.
+ * Arrays must be sized by the caller from that shape. */
+void oracle_fixture(uint32_t tokens, int permute, float* q, int64_t* qpos, int64_t* kpos,
+                    uint32_t* table, int8_t* k, int8_t* v, float* ks, float* vs) {
+  const uint32_t rows = 8, q_heads = 24, kv_heads = 4, dim = 256, P = 32;
+  const uint32_t pages = (tokens + P - 1) / P;
+  const size_t slots = (size_t)pages * kv_heads * P;
+  for (uint32_t p = 0; p < pages; ++p) table[p] = permute ? pages - 1 - p : p;
+  for (size_t i = 0; i < (size_t)rows * q_heads * dim; ++i)
+    q[i] = (float)((int)((i * 7) % 257) - 128) / 1024.0f;
+  for (uint32_t r = 0; r < rows; ++r) qpos[r] = (int64_t)tokens - rows + r;
+  memset(k, 0, slots * dim);
+  memset(v, 0, slots * dim);
+  for (size_t i = 0; i < slots; ++i) {
+    ks[i] = 1.0f;
+    vs[i] = 1.0f;
+  }
+  for (uint32_t t = 0; t < tokens; ++t) {
+    kpos[t] = t;
+    const uint32_t page = table[t / P], slot = t % P;
+    for (uint32_t h = 0; h < kv_heads; ++h) {
+      const size_t si = ((size_t)page * kv_heads + h) * P + slot;
+      ks[si] = (float)((t + h) % 7 + 1) / 512.0f;
+      vs[si] = (float)((t * 3 + h) % 5 + 1) / 512.0f;
+      for (uint32_t d = 0; d < dim; ++d) {
+        k[si * dim + d] = (int8_t)((int)((t * 17 + h * 11 + d * 3) % 256) - 128);
+        v[(((size_t)page * kv_heads + h) * dim + d) * P + slot] =
+            (int8_t)((int)((t * 7 + h * 13 + d * 5) % 256) - 128);
+      }
+    }
+  }
+}
