@@ -106,6 +106,14 @@ int kvb_decode_attention(const kvb_shape* s, const kvb_device_input* in, uint32_
  * these arguments: KVB_KERNEL_TILED_MFMA or KVB_KERNEL_GENERIC; 0 if invalid. */
 int kvb_selected_kernel(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens);
 
+/* Extension (diagnostic, no counterpart in the reference library): streams
+ * `bytes` (a multiple of 16) of device memory with non-temporal 16-byte loads
+ * over `blocks` work-groups of 256 threads, for measuring the device's
+ * achievable HBM read bandwidth next to the attention kernels (the role of the
+ * reference's stream probe, data/att-bench-65536-v2-07.json:528-541).  `sink`
+ * needs `blocks` uint32 and is practically never written. */
+int kvb_hbm_read_probe(const void* src, size_t bytes, uint32_t* sink, uint32_t blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,6 +11,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <stdexcept>
 #include <string>
 
@@ -67,7 +68,7 @@ int hip_status(hipError_t e, const char* op) {
 int run_split(const kvbridge::Shape& s, const kvbridge::DeviceInput& in, unsigned split_tokens,
               unsigned splits, float* scratch, hipStream_t stream, const char* op) {
   const kvb::SplitArgs a = kvb::make_split_args(s, in, split_tokens, splits, scratch);
-  const hipError_t e = kvb::tiled_supported(s, in) ? kvb::launch_split_tiled(a, stream)
+  const hipError_t e = kvb::tiled_supported(s, in) ? kvb::launch_split_fast(a, stream)
                                                    : kvb::launch_split_generic(a, s.int8, stream);
   return hip_status(e, op);
 }
@@ -121,6 +122,19 @@ SplitArgs make_split_args(const kvbridge::Shape& s, const kvbridge::DeviceInput&
   a.splits = splits;
   a.scale = s.scale;
   return a;
+}
+
+hipError_t launch_split_fast(const SplitArgs& a, hipStream_t stream) {
+  static const int impl = [] {  // 0 default, 1 f16 LDS, 2 register-staged
+    const char* e = std::getenv("KVB_SPLIT_IMPL");
+    if (!e) return 0;
+    if (std::string(e) == "f16") return 1;
+    if (std::string(e) == "reg") return 2;
+    return 0;
+  }();
+  if (impl == 2) return launch_split_tiled(a, stream);
+  if (impl == 0 && i8_supported(a)) return launch_split_i8(a, stream);
+  return launch_split_lds(a, stream);
 }
 
 bool tiled_supported(const kvbridge::Shape& s, const kvbridge::DeviceInput& in) {
@@ -322,6 +336,13 @@ int kvb_decode_attention(const kvb_shape* sp, const kvb_device_input* ip, uint32
     if (rc != KVB_OK) return rc;
     return run_merge(s, scratch, splits, m, l, n, out, out_type, st, "attention merge launch");
   });
+}
+
+int kvb_hbm_read_probe(const void* src, size_t bytes, uint32_t* sink, uint32_t blocks, void* stream) {
+  if (!src || !sink || bytes % 16 != 0 || blocks == 0)
+    return fail(KVB_EINVAL, "probe needs non-null 16-byte-multiple source, a sink and blocks > 0");
+  return hip_status(kvb::launch_read_probe(src, bytes, sink, blocks, static_cast<hipStream_t>(stream)),
+                    "read probe launch");
 }
 
 int kvb_selected_kernel(const kvb_shape* sp, const kvb_device_input* ip, uint32_t split_tokens) {

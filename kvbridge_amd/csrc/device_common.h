@@ -80,4 +80,28 @@ __device__ __forceinline__ f16x8 i8x8_to_f16(uint32_t lo, uint32_t hi) {
   return f16x8{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
 }
 
+// First t in [lo, hi) with kpos[t] > x, or hi (k_positions are nondecreasing).
+// 64-ary search by the whole wave: each round samples 64 evenly spaced
+// positions and keeps the sub-interval where the predicate flips.
+__device__ inline uint32_t visible_end(const int64_t* __restrict__ kpos, uint32_t lo, uint32_t hi, int64_t x,
+                                uint32_t lane) {
+  while (hi - lo > 64u) {
+    const uint32_t stride = (hi - lo + 63u) / 64u;
+    const uint64_t t = uint64_t(lo) + uint64_t(lane) * stride;
+    const bool p = t < hi && kpos[t] <= x;
+    const uint32_t c = uint32_t(__popcll(__ballot(p)));
+    if (c == 0) return lo;
+    const uint64_t nhi = uint64_t(lo) + uint64_t(c) * stride;
+    lo = lo + (c - 1u) * stride + 1u;
+    hi = nhi < hi ? uint32_t(nhi) : hi;
+  }
+  const uint32_t t = lo + lane;
+  const bool p = t < hi && kpos[t] <= x;
+  return lo + uint32_t(__popcll(__ballot(p)));
+}
+
+__device__ __forceinline__ uint32_t clampu(uint32_t x, uint32_t lo, uint32_t hi) {
+  return x < lo ? lo : (x > hi ? hi : x);
+}
+
 }  // namespace kvb

@@ -30,12 +30,23 @@ SplitArgs make_split_args(const kvbridge::Shape& s, const kvbridge::DeviceInput&
 // Whether the tiled MFMA split kernel covers this shape and these buffers.
 bool tiled_supported(const kvbridge::Shape& s, const kvbridge::DeviceInput& in);
 
-hipError_t launch_split_tiled(const SplitArgs& a, hipStream_t stream);
+hipError_t launch_split_tiled(const SplitArgs& a, hipStream_t stream);  // register-staged tiles
+hipError_t launch_split_lds(const SplitArgs& a, hipStream_t stream);    // LDS-DMA-staged tiles, f16 MFMA
+hipError_t launch_split_i8(const SplitArgs& a, hipStream_t stream);     // LDS-DMA-staged, int8 MFMA
+bool i8_supported(const SplitArgs& a);                                   // head_rows <= 8
+// The MFMA split path used by the entry points: the int8-MFMA kernel when
+// head_rows <= 8, else the f16-MFMA LDS kernel.  KVB_SPLIT_IMPL=f16 or =reg
+// forces the f16 LDS or the register-staged kernel (comparisons).
+hipError_t launch_split_fast(const SplitArgs& a, hipStream_t stream);
 hipError_t launch_split_generic(const SplitArgs& a, bool int8, hipStream_t stream);
 // out_type: 0 none, 1 fp32, 2 fp16 (kvbridge_c.h KVB_OUT_*).
 hipError_t launch_merge(uint32_t row_heads, uint32_t dim, uint32_t splits, const float* scratch,
                         float* m, float* l, float* n, void* out, int out_type,
                         hipStream_t stream);
+
+// Streaming HBM read probe (diagnostic).
+hipError_t launch_read_probe(const void* src, size_t bytes, uint32_t* sink, uint32_t blocks,
+                             hipStream_t stream);
 
 hipError_t preload_tiled();
 hipError_t preload_generic();

@@ -35,6 +35,8 @@
 // accumulator only ever needs an exact 2^-n rescale) and split into f16
 // hi + lo, giving ~22-bit weights against fp32 accumulation.  Softmax
 // reductions use DPP and permlane swaps, not LDS.
+#include <cstdlib>
+
 #include "kernels.h"
 #include "device_common.h"
 
@@ -50,8 +52,11 @@ struct Tile {
   float ks, vs;     // scales of token t0 + 16*g + lane%16
 };
 
+// Physical pages of the four 16-token groups of one tile.  Fetched with
+// wave-uniform addresses, so they are scalar loads (counted by lgkmcnt, not
+// vmcnt): waiting for them never waits for the tile loads in flight.
 struct Pages {
-  uint32_t k, v;  // physical pages of the lane's K-row group and of its own group g
+  uint32_t g[4];
 };
 
 struct WaveCtx {
@@ -61,51 +66,37 @@ struct WaveCtx {
   const float* __restrict__ vs;
   const uint32_t* __restrict__ table;
   uint32_t kv, kv_heads, P, pages;
-  uint32_t lp_lo, lp_hi;  // clamp range of logical pages (pages holding [s0, e_max))
+  uint32_t lp_lo, lp_hi;  // clamp range of logical pages (pages holding [s0, s1))
   uint32_t lane;
 };
 
-// First t in [lo, hi) with kpos[t] > x, or hi (k_positions are nondecreasing).
-// 64-ary search by the whole wave: each round samples 64 evenly spaced
-// positions and keeps the sub-interval where the predicate flips.
-__device__ uint32_t visible_end(const int64_t* __restrict__ kpos, uint32_t lo, uint32_t hi, int64_t x,
-                                uint32_t lane) {
-  while (hi - lo > 64u) {
-    const uint32_t stride = (hi - lo + 63u) / 64u;
-    const uint64_t t = uint64_t(lo) + uint64_t(lane) * stride;
-    const bool p = t < hi && kpos[t] <= x;
-    const uint32_t c = uint32_t(__popcll(__ballot(p)));
-    if (c == 0) return lo;
-    const uint64_t nhi = uint64_t(lo) + uint64_t(c) * stride;
-    lo = lo + (c - 1u) * stride + 1u;
-    hi = nhi < hi ? uint32_t(nhi) : hi;
-  }
-  const uint32_t t = lo + lane;
-  const bool p = t < hi && kpos[t] <= x;
-  return lo + uint32_t(__popcll(__ballot(p)));
-}
-
-__device__ __forceinline__ uint32_t clampu(uint32_t x, uint32_t lo, uint32_t hi) {
-  return x < lo ? lo : (x > hi ? hi : x);
-}
-
 __device__ __forceinline__ Pages fetch_pages(const WaveCtx& c, uint32_t tile) {
   const uint32_t t0 = tile * kTileTokens;
-  const uint32_t gk = (c.lane & 15u) >> 2, g = c.lane >> 4;
-  const uint32_t lk = clampu((t0 + 16u * gk) / c.P, c.lp_lo, c.lp_hi);
-  const uint32_t lv = clampu((t0 + 16u * g) / c.P, c.lp_lo, c.lp_hi);
   Pages p;
-  p.k = c.table[lk];
-  p.v = c.table[lv];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t lp = clampu((t0 + 16u * g) / c.P, c.lp_lo, c.lp_hi);
+    p.g[g] = c.table[lp];
+  }
   return p;
+}
+
+// The page of token group `grp` (0..3, per lane) from the four uniform
+// values, clamped into the pool (the clamp sits here, at the use, so that
+// fetching never waits for the scalar loads).
+__device__ __forceinline__ uint32_t pick(const Pages& p, uint32_t grp, uint32_t pages) {
+  const uint32_t lo = (grp & 1u) ? p.g[1] : p.g[0];
+  const uint32_t hi = (grp & 1u) ? p.g[3] : p.g[2];
+  const uint32_t x = (grp & 2u) ? hi : lo;
+  return x < pages ? x : pages - 1u;
 }
 
 template <int D>
 __device__ __forceinline__ void load_tile(Tile<D>& t, const WaveCtx& c, uint32_t tile, Pages pg) {
   const uint32_t t0 = tile * kTileTokens;
   const uint32_t lane = c.lane, g = lane >> 4, gk = (lane & 15u) >> 2;
-  const uint32_t pk = pg.k < c.pages ? pg.k : c.pages - 1u;
-  const uint32_t pv = pg.v < c.pages ? pg.v : c.pages - 1u;
+  const uint32_t pk = pick(pg, gk, c.pages);
+  const uint32_t pv = pick(pg, g, c.pages);
   // K: token row (t0 + 16*gk + 4*mb + lane%4), bytes [g*D/4, (g+1)*D/4).
   const uint32_t krow0 = (pk * c.kv_heads + c.kv) * c.P + (t0 + 16u * gk) % c.P + (lane & 3u);
   const int8_t* kp = c.kbase + size_t(krow0) * D + g * (D / 4);
@@ -238,12 +229,17 @@ __device__ __forceinline__ void compute_tile(State<D>& st, const Tile<D>& t, uin
 }
 
 template <int D, int NW>
-__global__ __launch_bounds__(64 * NW) void split_tiled_kernel(SplitArgs a) {
+__global__ __launch_bounds__(64 * NW) void split_tiled_kernel(
+    SplitArgs a, const float* __restrict__ q, const int64_t* __restrict__ qpos,
+    const int64_t* __restrict__ kpos, const uint32_t* __restrict__ table,
+    const int8_t* __restrict__ kdata, const int8_t* __restrict__ vdata,
+    const float* __restrict__ kscale, const float* __restrict__ vscale, float* __restrict__ scratch) {
   __shared__ float wm_s[NW][16];
   __shared__ float wl_s[NW][16];
   __shared__ float wacc_s[NW][16][D];
 
-  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t h = lane & 15u, g = lane >> 4;
   const uint32_t split = blockIdx.x;
   const uint32_t kv = blockIdx.y % a.kv_heads, hblock = blockIdx.y / a.kv_heads;
@@ -253,20 +249,63 @@ __global__ __launch_bounds__(64 * NW) void split_tiled_kernel(SplitArgs a) {
   const uint32_t row = hvalid ? hr / a.group : 0u;
   const uint32_t head = kv * a.group + (hvalid ? hr % a.group : 0u);
 
-  // Split interval [s0, s1).
+  // Split interval [s0, s1) and its tiles [k_first, k_last] (64-token tiles in
+  // absolute logical coordinates; boundary tiles are masked per token).
   const uint64_t s0_64 = uint64_t(a.begin) + uint64_t(split) * a.split_tokens;
   const uint32_t s0 = s0_64 < a.end ? uint32_t(s0_64) : a.end;
   const uint32_t s1 = uint64_t(s0) + a.split_tokens < a.end ? s0 + a.split_tokens : a.end;
+  const uint32_t k_first = s0 / kTileTokens;
+  const uint32_t k_last = s1 > s0 ? (s1 - 1u) / kTileTokens : k_first;
 
-  // Visible end per head-row: tokens [s0, e_h) are visible to this lane's row.
-  uint32_t e_h = s0;
+  WaveCtx c;
+  c.kbase = kdata;
+  c.vbase = vdata;
+  c.ks = kscale;
+  c.vs = vscale;
+  c.table = table;
+  c.kv = kv;
+  c.kv_heads = a.kv_heads;
+  c.P = a.page_tokens;
+  c.pages = a.pages;
+  c.lp_lo = s0 / a.page_tokens;
+  c.lp_hi = s1 > s0 ? (s1 - 1u) / a.page_tokens : c.lp_lo;
+  c.lane = lane;
+  auto tile_of = [&](uint32_t i) {  // i-th tile of this wave, clamped for harmless prefetch
+    const uint32_t k = k_first + wave + i * NW;
+    return k < k_last ? k : k_last;
+  };
+
+  // Start streaming this wave's first tile before anything else: the page
+  // entries and the KV loads do not depend on the visibility search below.
+  Tile<D> ta, tb;
+  const bool first = s1 > s0 && k_first + wave <= k_last;
+  Pages pb = {}, pc = {};
+  if (first) {
+    const Pages pa = fetch_pages(c, tile_of(0));
+    pb = fetch_pages(c, tile_of(1));
+    load_tile<D>(ta, c, tile_of(0), pa);
+    pc = fetch_pages(c, tile_of(2));
+  }
+
+  // Visible end per head-row: tokens [s0, e_h) are visible to this lane's row
+  // (k_positions are nondecreasing).  Common case: the last token of the split
+  // is visible to every row of the block, so nothing is searched.
   const uint32_t r_lo = hblock * 16u / a.group;
-  const uint32_t r_hi = ((hblock * 16u + 15u < head_rows ? hblock * 16u + 15u : head_rows - 1u)) / a.group;
+  const uint32_t r_hi = (hblock * 16u + 15u < head_rows ? hblock * 16u + 15u : head_rows - 1u) / a.group;
+  uint32_t e_h = s0;
   if (s1 > s0) {
-    for (uint32_t r = r_lo; r <= r_hi; ++r) {
-      const uint32_t e = visible_end(a.k_positions, s0, s1, a.q_positions[r], lane);
-      if (hvalid && row == r) e_h = e;
+    const int64_t klast = kpos[s1 - 1u];
+    bool all_visible = true;
+    for (uint32_t r = r_lo; r <= r_hi; ++r) all_visible &= klast <= qpos[r];
+    if (all_visible) {
+      e_h = s1;
+    } else {
+      for (uint32_t r = r_lo; r <= r_hi; ++r) {
+        const uint32_t e = visible_end(kpos, s0, s1, qpos[r], lane);
+        if (row == r) e_h = e;
+      }
     }
+    if (!hvalid) e_h = s0;
   }
   // Row-of-16 reductions (every row of lanes holds the same 16 head-rows).
   uint32_t e_min = hvalid ? e_h : 0xffffffffu, e_max = e_h;
@@ -285,7 +324,7 @@ __global__ __launch_bounds__(64 * NW) void split_tiled_kernel(SplitArgs a) {
   // Q of this head-row, dims [g*D/4, (g+1)*D/4), scaled by 2^kq into f16 hi/lo.
   float qv[D / 4];
   if (hvalid) {
-    const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t(row) * a.q_heads + head) * D + g * (D / 4));
+    const float4* qp = reinterpret_cast<const float4*>(q + (size_t(row) * a.q_heads + head) * D + g * (D / 4));
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) {
       const float4 x = qp[i];
@@ -327,59 +366,31 @@ __global__ __launch_bounds__(64 * NW) void split_tiled_kernel(SplitArgs a) {
   st.l = 0.f;
   st.kexp = 100;
 
-  if (e_max > s0) {
-    WaveCtx c;
-    c.kbase = static_cast<const int8_t*>(a.k);
-    c.vbase = static_cast<const int8_t*>(a.v);
-    c.ks = a.k_scales;
-    c.vs = a.v_scales;
-    c.table = a.page_table;
-    c.kv = kv;
-    c.kv_heads = a.kv_heads;
-    c.P = a.page_tokens;
-    c.pages = a.pages;
-    c.lp_lo = s0 / a.page_tokens;
-    c.lp_hi = (e_max - 1u) / a.page_tokens;
-    c.lane = lane;
-
-    const uint32_t k_first = s0 / kTileTokens;
-    const uint32_t k_count = (e_max - 1u) / kTileTokens + 1u - k_first;
-    const uint32_t nt = k_count > wave ? (k_count - wave + NW - 1u) / NW : 0u;
-    const uint32_t k_last = k_first + k_count - 1u;
-    auto tile_of = [&](uint32_t i) {  // i-th tile of this wave, clamped for harmless prefetch
-      const uint32_t k = k_first + wave + i * NW;
-      return k < k_last ? k : k_last;
-    };
-    auto is_full = [&](uint32_t k) {
-      return k * kTileTokens >= s0 && (k + 1u) * kTileTokens <= e_min;
-    };
-
-    if (nt > 0) {
-      Tile<D> ta, tb;
-      Pages pa = fetch_pages(c, tile_of(0));
-      Pages pb = fetch_pages(c, tile_of(1));
-      load_tile<D>(ta, c, tile_of(0), pa);
-      Pages pc = fetch_pages(c, tile_of(2));
-      for (uint32_t i = 0; i < nt; i += 2) {
-        // Invariant: ta holds (loads of) tile i; pb, pc are the pages of tiles i+1, i+2.
-        if (i + 1 < nt) load_tile<D>(tb, c, tile_of(i + 1), pb);
-        pa = fetch_pages(c, tile_of(i + 3));
-        {
-          const uint32_t k = tile_of(i);
-          compute_tile<D>(st, ta, k, qh, ql, qlo, cq, is_full(k), s0, e_h, e_max, lane);
-        }
-        if (i + 1 >= nt) break;
-        if (i + 2 < nt) load_tile<D>(ta, c, tile_of(i + 2), pc);
-        pb = fetch_pages(c, tile_of(i + 4));
-        {
-          const uint32_t k = tile_of(i + 1);
-          compute_tile<D>(st, tb, k, qh, ql, qlo, cq, is_full(k), s0, e_h, e_max, lane);
-        }
-        const Pages t3 = pa;
-        pc = pb;
-        pb = t3;
-      }
+  // Tiles holding visible tokens: [k_first, (e_max - 1) / 64]; the wave's
+  // first tile (already in flight) is the first of its round-robin share.
+  const uint32_t k_vis = e_max > s0 ? (e_max - 1u) / kTileTokens : 0u;
+  const uint32_t k_count = e_max > s0 ? k_vis + 1u - k_first : 0u;
+  const uint32_t nt = k_count > wave ? (k_count - wave + NW - 1u) / NW : 0u;
+  auto is_full = [&](uint32_t k) {
+    return k * kTileTokens >= s0 && (k + 1u) * kTileTokens <= e_min;
+  };
+  for (uint32_t i = 0; i < nt; i += 2) {
+    // Invariant: ta holds (loads of) tile i; pb, pc are the pages of tiles i+1, i+2.
+    if (i + 1 < nt) load_tile<D>(tb, c, tile_of(i + 1), pb);
+    const Pages pd = fetch_pages(c, tile_of(i + 3));
+    {
+      const uint32_t k = tile_of(i);
+      compute_tile<D>(st, ta, k, qh, ql, qlo, cq, is_full(k), s0, e_h, e_max, lane);
     }
+    if (i + 1 >= nt) break;
+    if (i + 2 < nt) load_tile<D>(ta, c, tile_of(i + 2), pc);
+    const Pages pe = fetch_pages(c, tile_of(i + 4));
+    {
+      const uint32_t k = tile_of(i + 1);
+      compute_tile<D>(st, tb, k, qh, ql, qlo, cq, is_full(k), s0, e_h, e_max, lane);
+    }
+    pb = pd;
+    pc = pe;
   }
 
   // ---- combine the waves through LDS and write the split partial.
@@ -419,9 +430,13 @@ __global__ __launch_bounds__(64 * NW) void split_tiled_kernel(SplitArgs a) {
     }
     const uint32_t hr2 = hblock * 16u + hh;
     const uint32_t row2 = hr2 / a.group, head2 = kv * a.group + hr2 % a.group;
-    a.scratch[((size_t(row2) * a.q_heads + head2) * a.splits + split) * W + col] = val;
+    scratch[((size_t(row2) * a.q_heads + head2) * a.splits + split) * W + col] = val;
   }
 }
+
+#define KVB_TILED_ARGS                                                                           \
+  a, a.q, a.q_positions, a.k_positions, a.page_table, static_cast<const int8_t*>(a.k),             \
+      static_cast<const int8_t*>(a.v), a.k_scales, a.v_scales, a.scratch
 
 // LDS holds one D-float numerator row per head-row and wave for the final
 // combine; NW is capped so that stays within 32 KiB.
@@ -434,15 +449,15 @@ hipError_t launch_d(const SplitArgs& a, int nw, hipStream_t stream) {
   const dim3 grid(a.splits, a.kv_heads * hblocks);
   if (nw > kMaxWaves<D>) nw = kMaxWaves<D>;
   switch (nw) {
-    case 1: hipLaunchKernelGGL((split_tiled_kernel<D, 1>), grid, dim3(64), 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((split_tiled_kernel<D, 2>), grid, dim3(128), 0, stream, a); break;
+    case 1: hipLaunchKernelGGL((split_tiled_kernel<D, 1>), grid, dim3(64), 0, stream, KVB_TILED_ARGS); break;
+    case 2: hipLaunchKernelGGL((split_tiled_kernel<D, 2>), grid, dim3(128), 0, stream, KVB_TILED_ARGS); break;
     case 4:
       if constexpr (kMaxWaves<D> >= 4)
-        hipLaunchKernelGGL((split_tiled_kernel<D, 4>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((split_tiled_kernel<D, 4>), grid, dim3(256), 0, stream, KVB_TILED_ARGS);
       break;
     default:
       if constexpr (kMaxWaves<D> >= 8)
-        hipLaunchKernelGGL((split_tiled_kernel<D, 8>), grid, dim3(512), 0, stream, a);
+        hipLaunchKernelGGL((split_tiled_kernel<D, 8>), grid, dim3(512), 0, stream, KVB_TILED_ARGS);
       break;
   }
   return hipGetLastError();
@@ -462,7 +477,13 @@ hipError_t preload_d() {
 }
 
 // Waves per work-group: enough tiles per wave to keep its double buffer busy.
+// KVB_TILED_WAVES (1, 2, 4, 8) overrides the choice, for tuning sweeps.
 int waves_for(const SplitArgs& a) {
+  static const int forced = [] {
+    const char* e = std::getenv("KVB_TILED_WAVES");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
   const uint32_t tiles = (a.split_tokens + kTileTokens - 1) / kTileTokens + 1u;
   if (tiles >= 32) return 4;
   if (tiles >= 12) return 2;
