@@ -15,7 +15,11 @@
  *                       patterned fixture)
  * Pinned by tests/test_oracle.py against the reference's own known-answer
  * tests (tests/reference_test.cpp), golden vectors produced by the
- * reference's FP64 oracle built from source (tests/golden), and closed forms. */
+ * reference's FP64 oracle built from source (tests/golden), and closed forms.
+ *
+ * oracle_set_fault() plants one known mistake (a dropped term, a wrong index
+ * or comparison) so the tests can show that their checks catch it; 0 (the
+ * default) is the faithful oracle. */
 #include "attention_oracle.h"
 
 #include <math.h>
@@ -23,20 +27,33 @@
 #include <stdlib.h>
 #include <string.h>
 
+static int g_fault = ORACLE_FAULT_NONE;
+void oracle_set_fault(int code) { g_fault = code; }
+
+static int visible_pos(int64_t kpos, int64_t qpos) {
+  return g_fault == ORACLE_FAULT_MASK_STRICT ? kpos < qpos : kpos <= qpos;
+}
+
 static double kv_at(const oracle_shape* s, const void* base, size_t i) {
   if (s->int8) return (double)((const int8_t*)base)[i];
   return (double)((const float*)base)[i];
 }
 
 /* Index of (physical page, kv head, slot) in the scale arrays; K row = this * dim. */
+static size_t page_of(const oracle_shape* s, const uint32_t* table, uint32_t t) {
+  return g_fault == ORACLE_FAULT_TABLE_IGNORED ? t / s->page_tokens : table[t / s->page_tokens];
+}
+
 static size_t slot_index(const oracle_shape* s, const uint32_t* table, uint32_t t, uint32_t kv) {
-  const size_t page = table[t / s->page_tokens];
+  const size_t page = page_of(s, table, t);
   return (page * s->kv_heads + kv) * s->page_tokens + t % s->page_tokens;
 }
 
 /* V element (d) of logical token t: V is dim-major inside a page. */
 static size_t v_index(const oracle_shape* s, const uint32_t* table, uint32_t t, uint32_t kv, uint32_t d) {
-  const size_t page = table[t / s->page_tokens];
+  const size_t page = page_of(s, table, t);
+  if (g_fault == ORACLE_FAULT_V_TOKEN_MAJOR)
+    return ((page * s->kv_heads + kv) * s->page_tokens + t % s->page_tokens) * s->dim + d;
   return ((page * s->kv_heads + kv) * s->dim + d) * s->page_tokens + t % s->page_tokens;
 }
 
@@ -51,13 +68,31 @@ typedef struct {
   uint32_t rh_begin, rh_end;
 } fp64_job;
 
+static uint32_t kv_of(const oracle_shape* s, uint32_t h) {
+  if (g_fault == ORACLE_FAULT_GQA_MODULO) return h % s->kv_heads;
+  return h / (s->q_heads / s->kv_heads);
+}
+
+static double kscale_of(const oracle_shape* s, const float* ks, size_t si) {
+  if (!s->int8 || g_fault == ORACLE_FAULT_KSCALE_DROPPED) return 1.0;
+  return (double)ks[si];
+}
+
+static double vscale_of(const oracle_shape* s, const float* vs, size_t si) {
+  if (!s->int8 || g_fault == ORACLE_FAULT_VSCALE_DROPPED) return 1.0;
+  return (double)vs[si];
+}
+
+static double score_scale(const oracle_shape* s) {
+  return g_fault == ORACLE_FAULT_SCALE_DROPPED ? 1.0 : (double)s->scale;
+}
+
 static void fp64_rows(const fp64_job* j) {
   const oracle_shape* s = j->s;
-  const uint32_t group = s->q_heads / s->kv_heads;
   const uint32_t n = s->end - s->begin;
   double* logits = (double*)malloc(sizeof(double) * (n ? n : 1));
   for (uint32_t rh = j->rh_begin; rh < j->rh_end; ++rh) {
-    const uint32_t r = rh / s->q_heads, h = rh % s->q_heads, kv = h / group;
+    const uint32_t r = rh / s->q_heads, h = rh % s->q_heads, kv = kv_of(s, h);
     const float* q = j->q + (size_t)rh * s->dim;
     double* o = j->out + (size_t)rh * s->dim;
     double mx = -INFINITY;
@@ -65,12 +100,12 @@ static void fp64_rows(const fp64_job* j) {
     for (uint32_t d = 0; d < s->dim; ++d) o[d] = 0.0;
     for (uint32_t t = s->begin; t < s->end; ++t) {
       double lg = -INFINITY;
-      if (j->kpos[t] <= j->qpos[r]) {
+      if (visible_pos(j->kpos[t], j->qpos[r])) {
         const size_t si = slot_index(s, j->table, t, kv);
-        const double ks = s->int8 ? (double)j->ks[si] : 1.0;
+        const double ks = kscale_of(s, j->ks, si);
         double dot = 0.0;
         for (uint32_t d = 0; d < s->dim; ++d) dot += (double)q[d] * kv_at(s, j->k, si * s->dim + d) * ks;
-        lg = dot * (double)s->scale;
+        lg = dot * score_scale(s);
         any = 1;
       }
       logits[t - s->begin] = lg;
@@ -84,7 +119,7 @@ static void fp64_rows(const fp64_job* j) {
       if (w == 0.0) continue;
       den += w;
       const size_t si = slot_index(s, j->table, t, kv);
-      const double vs = s->int8 ? (double)j->vs[si] : 1.0;
+      const double vs = vscale_of(s, j->vs, si);
       for (uint32_t d = 0; d < s->dim; ++d) o[d] += w * kv_at(s, j->v, v_index(s, j->table, t, kv, d)) * vs;
     }
     for (uint32_t d = 0; d < s->dim; ++d) o[d] /= den;
@@ -135,31 +170,31 @@ typedef struct {
 
 static void split_units(const split_job* j) {
   const oracle_shape* s = j->s;
-  const uint32_t group = s->q_heads / s->kv_heads;
   const uint32_t stride = s->dim + 2;
   float* w = (float*)malloc(sizeof(float) * (j->split_tokens ? j->split_tokens : 1));
   for (uint32_t u = j->unit_begin; u < j->unit_end; ++u) {
     const uint32_t rh = u / j->splits, split = u % j->splits;
-    const uint32_t r = rh / s->q_heads, h = rh % s->q_heads, kv = h / group;
+    const uint32_t r = rh / s->q_heads, h = rh % s->q_heads, kv = kv_of(s, h);
     const float* q = j->q + (size_t)rh * s->dim;
     float* part = j->scratch + (size_t)u * stride;
-    const uint64_t start64 = (uint64_t)s->begin + (uint64_t)split * j->split_tokens;
+    const uint64_t start64 = (g_fault == ORACLE_FAULT_SPLIT_IGNORES_BEGIN ? 0u : (uint64_t)s->begin) +
+                             (uint64_t)split * j->split_tokens;
     const uint32_t start = start64 < s->end ? (uint32_t)start64 : s->end;
     const uint32_t count = (uint64_t)s->end - start < j->split_tokens ? s->end - start : j->split_tokens;
     float mx = -INFINITY;
     for (uint32_t i = 0; i < count; ++i) {
       const uint32_t t = start + i;
       float sc = -INFINITY;
-      if (j->kpos[t] <= j->qpos[r]) {
+      if (visible_pos(j->kpos[t], j->qpos[r])) {
         const size_t si = slot_index(s, j->table, t, kv);
-        const float kscale = s->int8 ? j->ks[si] : 1.0f;
+        const float kscale = (float)kscale_of(s, j->ks, si);
         float dot = 0.0f;
         for (uint32_t d = 0; d < s->dim; ++d) {
           const float kf = s->int8 ? (float)((const int8_t*)j->k)[si * s->dim + d] * kscale
                                    : ((const float*)j->k)[si * s->dim + d];
           dot = fmaf(q[d], kf, dot);
         }
-        sc = dot * s->scale;
+        sc = dot * (float)score_scale(s);
       }
       w[i] = sc;
       if (sc > mx) mx = sc;
@@ -172,7 +207,7 @@ static void split_units(const split_job* j) {
       if (wt == 0.0f) continue;
       const uint32_t t = start + i;
       const size_t si = slot_index(s, j->table, t, kv);
-      const float wsc = wt * (s->int8 ? j->vs[si] : 1.0f);
+      const float wsc = wt * (float)vscale_of(s, j->vs, si);
       for (uint32_t d = 0; d < s->dim; ++d) {
         const size_t vi = v_index(s, j->table, t, kv, d);
         const float vf = s->int8 ? (float)((const int8_t*)j->v)[vi] : ((const float*)j->v)[vi];
@@ -226,7 +261,7 @@ void oracle_merge_fp32(const oracle_shape* s, const float* scratch, uint32_t spl
     for (uint32_t d = 0; d < s->dim; ++d) n[(size_t)rh * s->dim + d] = 0.0f;
     for (uint32_t j = 0; j < splits; ++j) {
       const float* p = base + (size_t)j * stride;
-      if (!(p[1] > 0.0f)) continue;
+      if (!(p[1] > 0.0f) && g_fault != ORACLE_FAULT_MERGE_NO_SKIP) continue;
       const float f = expf(p[0] - mx);
       den += f * p[1];
       for (uint32_t d = 0; d < s->dim; ++d)

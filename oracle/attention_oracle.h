@@ -38,6 +38,22 @@ void oracle_merge_fp32(const oracle_shape* s, const float* scratch, uint32_t spl
 void oracle_fixture(uint32_t tokens, int permute, float* q, int64_t* qpos, int64_t* kpos,
                     uint32_t* table, int8_t* k, int8_t* v, float* ks, float* vs);
 
+/* Planted mistakes for the tests that show the oracle's checks have teeth.
+ * Process-global; 0 restores the faithful oracle. */
+enum {
+  ORACLE_FAULT_NONE = 0,
+  ORACLE_FAULT_KSCALE_DROPPED = 1,   /* k-scale not applied to the dot        */
+  ORACLE_FAULT_VSCALE_DROPPED = 2,   /* v-scale not applied to V              */
+  ORACLE_FAULT_SCALE_DROPPED = 3,    /* score scale not applied               */
+  ORACLE_FAULT_MASK_STRICT = 4,      /* kpos < qpos instead of kpos <= qpos   */
+  ORACLE_FAULT_TABLE_IGNORED = 5,    /* logical page used as physical page    */
+  ORACLE_FAULT_V_TOKEN_MAJOR = 6,    /* V read token-major (transposed)       */
+  ORACLE_FAULT_GQA_MODULO = 7,       /* kv head = h % kv_heads                */
+  ORACLE_FAULT_SPLIT_IGNORES_BEGIN = 8, /* splits start at 0, not at begin    */
+  ORACLE_FAULT_MERGE_NO_SKIP = 9     /* merge does not skip l <= 0 splits     */
+};
+void oracle_set_fault(int code);
+
 #ifdef __cplusplus
 }
 #endif

@@ -40,6 +40,25 @@ def lib():
     return _lib
 
 
+# Planted mistakes (attention_oracle.h ORACLE_FAULT_*), for the tests that
+# show the oracle's checks catch them.
+FAULTS = {
+    "kscale_dropped": 1,
+    "vscale_dropped": 2,
+    "scale_dropped": 3,
+    "mask_strict": 4,
+    "table_ignored": 5,
+    "v_token_major": 6,
+    "gqa_modulo": 7,
+    "split_ignores_begin": 8,
+    "merge_no_skip": 9,
+}
+
+
+def set_fault(code: int) -> None:
+    lib().oracle_set_fault(ctypes.c_int(code))
+
+
 def ref_available() -> bool:
     return os.path.exists(REF_SO)
 
