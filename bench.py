@@ -46,6 +46,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="skip the hipGraph replay (profiling runs)")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run known-size copy and read kernels (for scaling rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
@@ -83,6 +86,7 @@ def main():
     n = torch.empty(rh * D, dtype=torch.float32, device=dev)
     out = torch.empty(rh * D, dtype=torch.float16, device=dev)
     assert kvb.selected_kernel(s, inps[0], st) == kvb.KVB_KERNEL_TILED_MFMA
+    split_kernel = kvb.selected_kernel_name(s, inps[0], st)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
 
@@ -125,28 +129,33 @@ def main():
     eager_ms = e0.elapsed_time(e1) / args.steps
 
     # ---- hipGraph replay: one graph holds one call per KV copy
-    graph = torch.cuda.CUDAGraph()
-    gs = torch.cuda.Stream()
-    gs.wait_stream(stream)
-    with torch.cuda.stream(gs):
-        call(0)  # warm the capture stream
-    torch.cuda.synchronize()
-    with torch.cuda.graph(graph, stream=gs):
-        for c in range(len(inps)):
-            kvb.decode_attention(s, inps[c], st, scratch, m, l, n, out, kvb.KVB_OUT_F16, gs.cuda_stream)
-    torch.cuda.synchronize()
-    reps = max(1, args.steps // len(inps))
-    for _ in range(3):
-        graph.replay()
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(reps):
-        graph.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    graph_ms = e0.elapsed_time(e1) / (reps * len(inps))
+    graph_ms = None
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        gs = torch.cuda.Stream()
+        gs.wait_stream(stream)
+        with torch.cuda.stream(gs):
+            call(0)  # warm the capture stream
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=gs):
+            for c in range(len(inps)):
+                kvb.decode_attention(s, inps[c], st, scratch, m, l, n, out, kvb.KVB_OUT_F16, gs.cuda_stream)
+        torch.cuda.synchronize()
+        reps = max(1, args.steps // len(inps))
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        graph_ms = e0.elapsed_time(e1) / (reps * len(inps))
 
-    # ---- split kernel alone (dominant kernel), events on its launch stream
+    # ---- split kernel alone (dominant kernel): HIP events on its launch
+    # stream around back-to-back launches (the average agrees with the
+    # rocprofv3 kernel-trace average; events around single launches add
+    # several µs of event overhead each).
     def split_only(i):
         kvb.split_attention(s, inps[i % len(inps)], st, scratch, sp)
 
@@ -170,11 +179,32 @@ def main():
 
     # The headline call time is the graph-replayed one (what a decode loop
     # that captures its step sees); the eager number is reported beside it.
-    call_ms = graph_ms
+    call_ms = graph_ms if graph_ms is not None else eager_ms
     value = kv_bytes / (call_ms * 1e-3) / 1e9
     split_gbs = kv_bytes / (split_ms * 1e-3) / 1e9
-    log(f"eager {eager_ms*1e3:.2f} us/call, graph {graph_ms*1e3:.2f} us/call, "
-        f"split-only {split_ms*1e3:.2f} us ({split_gbs:.0f} GB/s), merge-only {merge_ms*1e3:.2f} us")
+    log(f"eager {eager_ms*1e3:.2f} us/call, graph {graph_ms*1e3 if graph_ms else float('nan'):.2f} us/call, "
+        f"{split_kernel} {split_ms*1e3:.2f} us/launch ({split_gbs:.0f} GB/s), merge-only {merge_ms*1e3:.2f} us")
+
+    # ---- known-size kernels for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE
+    if args.calibrate:
+        cal_bytes = 256 << 20
+        src = torch.empty(cal_bytes, dtype=torch.uint8, device=dev)
+        dst = torch.empty(cal_bytes, dtype=torch.uint8, device=dev)
+        sink = torch.zeros(8192, dtype=torch.int32, device=dev)
+        for _ in range(5):
+            dst.copy_(src)                                   # reads and writes cal_bytes
+            kvb.hbm_read_probe(src, cal_bytes, sink, 4096)   # reads cal_bytes
+        torch.cuda.synchronize()
+        log(f"calibration: 5 x copy of {cal_bytes} B and 5 x read probe of {cal_bytes} B")
+
+    # ---- HBM traffic per split launch, from committed rocprofv3 counter runs
+    traffic = None
+    tpath = os.path.join(root, "profiles", "traffic_cfg2.json")
+    if os.path.exists(tpath):
+        with open(tpath) as fh:
+            tinfo = json.load(fh)
+        if tinfo.get("kernel") == split_kernel:
+            traffic = tinfo.get("hbm_bytes_per_launch")
 
     # ---- CPU baseline: the reference's FP64 oracle on this host
     cpu = None
@@ -206,21 +236,22 @@ def main():
         "us_per_call": round(call_ms * 1e3, 3),
         "pct_of_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "eager_us_per_call": round(eager_ms * 1e3, 3),
-        "graph_us_per_call": round(graph_ms * 1e3, 3),
+        "graph_us_per_call": round(graph_ms * 1e3, 3) if graph_ms is not None else None,
         "split_kernel_us": round(split_ms * 1e3, 3),
         "merge_kernel_us": round(merge_ms * 1e3, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 KV codes, f16 MFMA, fp32 accumulate",
+        "dtype": "i8",
         "data": "synthetic",
         "config": {"workload": "cfg2: 1 seq, 32q/8kv heads, d128, 65536 tokens, page 64, random 1024-page "
                                "permutation, int8 KV + per-(token,kv_head) fp32 scales, 32 splits, fp16 out",
                    "kv_copies_rotated": args.copies, "kv_bytes_per_call": kv_bytes, "split_tokens": st,
                    "splits": splits},
         "roofline": {"bound": "hbm", "achieved": round(split_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(split_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "split_tiled_kernel<128,4>", "algorithmic_bytes_per_launch": kv_bytes},
+                     "frac": round(split_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": split_kernel, "algorithmic_bytes_per_launch": kv_bytes,
+                     "launch_us": round(split_ms * 1e3, 3)},
         "cpu_baseline": cpu,
         "parity": parity,
     }

@@ -152,6 +152,10 @@ def selected_kernel(s: Shape, inp: DeviceInput, split_tokens: int) -> int:
     return load().kvb_selected_kernel(ctypes.byref(s), ctypes.byref(inp), split_tokens)
 
 
+def selected_kernel_name(s: Shape, inp: DeviceInput, split_tokens: int) -> str:
+    return load().kvb_selected_kernel_name(ctypes.byref(s), ctypes.byref(inp), split_tokens).decode()
+
+
 def hbm_read_probe(src, nbytes: int, sink, blocks: int, stream=None) -> None:
     """Diagnostic streaming read of nbytes of device memory (see kvb_hbm_read_probe)."""
     check(load().kvb_hbm_read_probe(_ptr(src), nbytes, _ptr(sink), blocks, _stream(stream)))

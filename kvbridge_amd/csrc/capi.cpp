@@ -124,17 +124,23 @@ SplitArgs make_split_args(const kvbridge::Shape& s, const kvbridge::DeviceInput&
   return a;
 }
 
-hipError_t launch_split_fast(const SplitArgs& a, hipStream_t stream) {
-  static const int impl = [] {  // 0 default, 1 f16 LDS, 2 register-staged
+static bool force_f16() {
+  static const bool f = [] {
     const char* e = std::getenv("KVB_SPLIT_IMPL");
-    if (!e) return 0;
-    if (std::string(e) == "f16") return 1;
-    if (std::string(e) == "reg") return 2;
-    return 0;
+    return e && std::string(e) == "f16";
   }();
-  if (impl == 2) return launch_split_tiled(a, stream);
-  if (impl == 0 && i8_supported(a)) return launch_split_i8(a, stream);
+  return f;
+}
+
+hipError_t launch_split_fast(const SplitArgs& a, hipStream_t stream) {
+  if (!force_f16() && i8_supported(a)) return launch_split_i8(a, stream);
   return launch_split_lds(a, stream);
+}
+
+const char* split_kernel_name(const SplitArgs& a, bool tiled, bool int8) {
+  if (!tiled) return int8 ? "split_generic_kernel<true>" : "split_generic_kernel<false>";
+  if (!force_f16() && i8_supported(a)) return i8_kernel_name(a);
+  return lds_kernel_name(a);
 }
 
 bool tiled_supported(const kvbridge::Shape& s, const kvbridge::DeviceInput& in) {
@@ -202,7 +208,8 @@ int kvb_mma_supported(const kvb_shape* s) {
 
 int kvb_preload_attention_reference_kernels(void) {
   hipError_t e = kvb::preload_generic();
-  if (e == hipSuccess) e = kvb::preload_tiled();
+  if (e == hipSuccess) e = kvb::preload_i8();
+  if (e == hipSuccess) e = kvb::preload_lds();
   if (e == hipSuccess) e = kvb::preload_merge();
   return int(e);
 }
@@ -214,7 +221,7 @@ int kvb_preload_attention_mma_kernels(void) {
   int device = 0;
   hipError_t e = hipGetDevice(&device);
   if (e != hipSuccess) return int(e);
-  e = kvb::preload_tiled();
+  e = kvb::preload_lds();
   if (e == hipSuccess) e = kvb::preload_merge();
   return int(e);
 }
@@ -350,6 +357,21 @@ int kvb_selected_kernel(const kvb_shape* sp, const kvb_device_input* ip, uint32_
   const kvbridge::Shape s = to_shape(*sp);
   if (!kvbridge::attention_shape_valid(s)) return 0;
   return kvb::tiled_supported(s, to_input(*ip)) ? KVB_KERNEL_TILED_MFMA : KVB_KERNEL_GENERIC;
+}
+
+const char* kvb_selected_kernel_name(const kvb_shape* sp, const kvb_device_input* ip, uint32_t split_tokens) {
+  if (!sp || !ip || split_tokens == 0) return "";
+  const kvbridge::Shape s = to_shape(*sp);
+  if (!kvbridge::attention_shape_valid(s)) return "";
+  const kvbridge::DeviceInput in = to_input(*ip);
+  unsigned splits = 0;
+  try {
+    splits = kvbridge::split_count(s, split_tokens);
+  } catch (...) {
+    return "";
+  }
+  const kvb::SplitArgs a = kvb::make_split_args(s, in, split_tokens, splits, nullptr);
+  return kvb::split_kernel_name(a, kvb::tiled_supported(s, in), s.int8);
 }
 
 }  // extern "C"

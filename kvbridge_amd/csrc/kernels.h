@@ -27,18 +27,21 @@ struct SplitArgs {
 SplitArgs make_split_args(const kvbridge::Shape& s, const kvbridge::DeviceInput& in,
                           unsigned split_tokens, unsigned splits, float* scratch);
 
-// Whether the tiled MFMA split kernel covers this shape and these buffers.
+// Whether the tiled MFMA split kernels cover this shape and these buffers.
 bool tiled_supported(const kvbridge::Shape& s, const kvbridge::DeviceInput& in);
 
-hipError_t launch_split_tiled(const SplitArgs& a, hipStream_t stream);  // register-staged tiles
-hipError_t launch_split_lds(const SplitArgs& a, hipStream_t stream);    // LDS-DMA-staged tiles, f16 MFMA
-hipError_t launch_split_i8(const SplitArgs& a, hipStream_t stream);     // LDS-DMA-staged, int8 MFMA
-bool i8_supported(const SplitArgs& a);                                   // head_rows <= 8
-// The MFMA split path used by the entry points: the int8-MFMA kernel when
-// head_rows <= 8, else the f16-MFMA LDS kernel.  KVB_SPLIT_IMPL=f16 or =reg
-// forces the f16 LDS or the register-staged kernel (comparisons).
+hipError_t launch_split_lds(const SplitArgs& a, hipStream_t stream);  // LDS-DMA-staged tiles, f16 MFMA
+hipError_t launch_split_i8(const SplitArgs& a, hipStream_t stream);   // register-staged tiles, int8 MFMA
+bool i8_supported(const SplitArgs& a);  // head_rows <= 8 (<= 4 at dim 256), power-of-two pages
+// The MFMA split path used by the entry points: the int8-MFMA kernel where
+// i8_supported, else the f16-MFMA LDS kernel.  KVB_SPLIT_IMPL=f16 forces the
+// f16 kernel (comparisons).
 hipError_t launch_split_fast(const SplitArgs& a, hipStream_t stream);
 hipError_t launch_split_generic(const SplitArgs& a, bool int8, hipStream_t stream);
+// Kernel instance a launch would run (diagnostics, profiles).
+const char* lds_kernel_name(const SplitArgs& a);
+const char* i8_kernel_name(const SplitArgs& a);
+const char* split_kernel_name(const SplitArgs& a, bool tiled, bool int8);
 // out_type: 0 none, 1 fp32, 2 fp16 (kvbridge_c.h KVB_OUT_*).
 hipError_t launch_merge(uint32_t row_heads, uint32_t dim, uint32_t splits, const float* scratch,
                         float* m, float* l, float* n, void* out, int out_type,
@@ -48,7 +51,8 @@ hipError_t launch_merge(uint32_t row_heads, uint32_t dim, uint32_t splits, const
 hipError_t launch_read_probe(const void* src, size_t bytes, uint32_t* sink, uint32_t blocks,
                              hipStream_t stream);
 
-hipError_t preload_tiled();
+hipError_t preload_lds();
+hipError_t preload_i8();
 hipError_t preload_generic();
 hipError_t preload_merge();
 

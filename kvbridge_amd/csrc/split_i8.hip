@@ -37,6 +37,7 @@
 // scratch[((row*q_heads + head)*splits + split)*(dim+2) + col], col 0 = split
 // max score (natural log units), 1 = sum of exp(score - max), 2.. =
 // sum of exp(score - max) * v_scale * v_code.
+#include <cstdio>
 #include <cstdlib>
 
 #include "kernels.h"
@@ -601,21 +602,38 @@ hipError_t launch_i8(const SplitArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <int D, int NW, int HS>
+hipError_t preload_hs() {
+  hipFuncAttributes attr{};
+  hipError_t e = hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_i8_kernel<D, NW, 2, true, HS>));
+  if (e != hipSuccess) return e;
+  return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_i8_kernel<D, NW, 2, false, HS>));
+}
+
 // Waves per work-group by tiles per split; eight waves (two per SIMD, <= 256
-// registers each) only where the state fits.  KVB_I8_WAVES (2, 4, 8) overrides.
-template <int D, int HS>
-hipError_t launch_hs(const SplitArgs& a, hipStream_t stream) {
+// registers each) only where the state fits (HS <= 4, dim <= 128).
+// KVB_I8_WAVES (2, 4, 8) overrides (tuning sweeps).
+int i8_waves(const SplitArgs& a) {
   static const int forced = [] {
     const char* e = std::getenv("KVB_I8_WAVES");
     return e ? std::atoi(e) : 0;
   }();
   const uint32_t tiles = (a.split_tokens + kTileTokens - 1) / kTileTokens;
-  const int nw = forced ? forced : (tiles >= 16 ? 8 : (tiles >= 4 ? 4 : 2));
+  int nw = forced ? forced : (tiles >= 16 ? 8 : (tiles >= 4 ? 4 : 2));
+  nw = nw >= 8 ? 8 : (nw >= 4 ? 4 : 2);
+  const bool small = a.rows * a.group <= 4;
+  if (nw == 8 && !(small && a.dim <= 128)) nw = 4;
+  return nw;
+}
+
+template <int D, int HS>
+hipError_t launch_hs(const SplitArgs& a, hipStream_t stream) {
   constexpr int NB = 2;
+  const int nw = i8_waves(a);
   if constexpr (HS <= 4 && D <= 128) {
-    if (nw >= 8) return launch_i8<D, 8, NB, HS>(a, stream);
+    if (nw == 8) return launch_i8<D, 8, NB, HS>(a, stream);
   }
-  if (nw >= 4) return launch_i8<D, 4, NB, HS>(a, stream);
+  if (nw == 4) return launch_i8<D, 4, NB, HS>(a, stream);
   return launch_i8<D, 2, NB, HS>(a, stream);
 }
 
@@ -639,6 +657,29 @@ hipError_t launch_split_i8(const SplitArgs& a, hipStream_t stream) {
     case 256: return launch_hs<256, 4>(a, stream);
     default: return hipErrorInvalidValue;
   }
+}
+
+const char* i8_kernel_name(const SplitArgs& a) {
+  static thread_local char buf[96];
+  std::snprintf(buf, sizeof(buf), "split_i8_kernel<%u,%d,2,%s,%d>", a.dim, i8_waves(a),
+                a.page_tokens >= kTileTokens ? "true" : "false", a.rows * a.group <= 4 ? 4 : 8);
+  return buf;
+}
+
+hipError_t preload_i8() {
+  hipError_t e;
+  if ((e = preload_hs<64, 8, 4>()) != hipSuccess) return e;
+  if ((e = preload_hs<64, 4, 4>()) != hipSuccess) return e;
+  if ((e = preload_hs<64, 2, 4>()) != hipSuccess) return e;
+  if ((e = preload_hs<64, 4, 8>()) != hipSuccess) return e;
+  if ((e = preload_hs<64, 2, 8>()) != hipSuccess) return e;
+  if ((e = preload_hs<128, 8, 4>()) != hipSuccess) return e;
+  if ((e = preload_hs<128, 4, 4>()) != hipSuccess) return e;
+  if ((e = preload_hs<128, 2, 4>()) != hipSuccess) return e;
+  if ((e = preload_hs<128, 4, 8>()) != hipSuccess) return e;
+  if ((e = preload_hs<128, 2, 8>()) != hipSuccess) return e;
+  if ((e = preload_hs<256, 4, 4>()) != hipSuccess) return e;
+  return preload_hs<256, 2, 4>();
 }
 
 }  // namespace kvb

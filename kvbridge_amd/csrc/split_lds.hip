@@ -22,6 +22,7 @@
 // Tile buffer (bytes):  K [64 tokens][D]   row r at r*D, chunk c at 16*(c ^ fK(r))
 //                       V [D dims][64 B]   row d at d*64, chunk c at 16*(c ^ fV(d))
 //                       k-scales [64], v-scales [64] floats, token order.
+#include <cstdio>
 #include <cstdlib>
 #include <type_traits>
 
@@ -423,11 +424,18 @@ hipError_t launch_cfg(const SplitArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-}  // namespace
+template <int D, int NW, int NB>
+hipError_t preload_cfg() {
+  hipFuncAttributes attr{};
+  hipError_t e = hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_lds_kernel<D, NW, NB, true>));
+  if (e != hipSuccess) return e;
+  return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_lds_kernel<D, NW, NB, false>));
+}
 
-// (waves, buffers) per work-group by dim and tiles per split; LDS use is
-// NW * NB * (128 * D + 512) bytes.  KVB_LDS_CFG="NW,NB" overrides (tuning).
-hipError_t launch_split_lds(const SplitArgs& a, hipStream_t stream) {
+// (waves, buffers) per work-group by dim and tiles per split, as 10*NW + NB;
+// LDS use is NW * NB * (128 * D + 512) bytes.  KVB_LDS_CFG="NW,NB" overrides
+// (tuning sweeps).
+int lds_config(const SplitArgs& a) {
   static const int forced = [] {
     const char* e = std::getenv("KVB_LDS_CFG");
     if (!e) return 0;
@@ -436,30 +444,52 @@ hipError_t launch_split_lds(const SplitArgs& a, hipStream_t stream) {
   const uint32_t tiles = (a.split_tokens + kTileTokens - 1) / kTileTokens;
   int cfg = forced;
   if (a.dim == 128) {
-    if (!cfg) cfg = tiles >= 16 ? 42 : 41;
-    switch (cfg) {
-      case 41: return launch_cfg<128, 4, 1>(a, stream);
-      case 81: return launch_cfg<128, 8, 1>(a, stream);
-      case 23: return launch_cfg<128, 2, 3>(a, stream);
-      default: return launch_cfg<128, 4, 2>(a, stream);
-    }
+    if (cfg != 41 && cfg != 81 && cfg != 23 && cfg != 42) cfg = tiles >= 16 ? 42 : 41;
+  } else if (a.dim == 64) {
+    if (cfg != 41 && cfg != 42 && cfg != 43) cfg = tiles >= 16 ? 43 : 41;
+  } else {
+    if (cfg != 41 && cfg != 22) cfg = tiles >= 16 ? 22 : 41;
   }
-  if (a.dim == 64) {
-    if (!cfg) cfg = tiles >= 16 ? 43 : 41;
-    switch (cfg) {
-      case 41: return launch_cfg<64, 4, 1>(a, stream);
-      case 42: return launch_cfg<64, 4, 2>(a, stream);
-      default: return launch_cfg<64, 4, 3>(a, stream);
-    }
+  return cfg;
+}
+
+}  // namespace
+
+hipError_t launch_split_lds(const SplitArgs& a, hipStream_t stream) {
+  const int cfg = lds_config(a);
+  switch (a.dim * 100 + cfg) {
+    case 12841: return launch_cfg<128, 4, 1>(a, stream);
+    case 12881: return launch_cfg<128, 8, 1>(a, stream);
+    case 12823: return launch_cfg<128, 2, 3>(a, stream);
+    case 12842: return launch_cfg<128, 4, 2>(a, stream);
+    case 6441: return launch_cfg<64, 4, 1>(a, stream);
+    case 6442: return launch_cfg<64, 4, 2>(a, stream);
+    case 6443: return launch_cfg<64, 4, 3>(a, stream);
+    case 25641: return launch_cfg<256, 4, 1>(a, stream);
+    case 25622: return launch_cfg<256, 2, 2>(a, stream);
+    default: return hipErrorInvalidValue;
   }
-  if (a.dim == 256) {
-    if (!cfg) cfg = tiles >= 16 ? 22 : 41;
-    switch (cfg) {
-      case 41: return launch_cfg<256, 4, 1>(a, stream);
-      default: return launch_cfg<256, 2, 2>(a, stream);
-    }
-  }
-  return hipErrorInvalidValue;
+}
+
+const char* lds_kernel_name(const SplitArgs& a) {
+  static thread_local char buf[96];
+  const int cfg = lds_config(a);
+  std::snprintf(buf, sizeof(buf), "split_lds_kernel<%u,%d,%d,%s>", a.dim, cfg / 10, cfg % 10,
+                a.page_tokens % kTileTokens == 0 ? "true" : "false");
+  return buf;
+}
+
+hipError_t preload_lds() {
+  hipError_t e;
+  if ((e = preload_cfg<128, 4, 1>()) != hipSuccess) return e;
+  if ((e = preload_cfg<128, 8, 1>()) != hipSuccess) return e;
+  if ((e = preload_cfg<128, 2, 3>()) != hipSuccess) return e;
+  if ((e = preload_cfg<128, 4, 2>()) != hipSuccess) return e;
+  if ((e = preload_cfg<64, 4, 1>()) != hipSuccess) return e;
+  if ((e = preload_cfg<64, 4, 2>()) != hipSuccess) return e;
+  if ((e = preload_cfg<64, 4, 3>()) != hipSuccess) return e;
+  if ((e = preload_cfg<256, 4, 1>()) != hipSuccess) return e;
+  return preload_cfg<256, 2, 2>();
 }
 
 }  // namespace kvb
