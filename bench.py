@@ -5,8 +5,10 @@ Workload: 1 sequence, 32 query heads / 8 KV heads
 (GQA 4), head_dim 128, 65536-token context, page size 64, page table a seeded
 random permutation of the 1024-page pool, INT8 K/V with per-(token, kv_head)
 fp32 scales, fp16-exact Q, 32 splits (2048 tokens each), fp32 partials, LSE
-merge, fp16 output.  A step is one decode-attention call: split kernel +
-merge/normalize kernel through the C ABI (kvb_decode_attention).
+merge, fp16 output.  A step is one decode-attention call through the C ABI:
+kvb_decode_attention_fused (one launch: the int8-MFMA split kernel, whose
+last work-group per kv head merges and normalizes).  The two-launch
+kvb_decode_attention (split kernel + merge kernel) is timed beside it.
 
 Inputs are resident in HBM before timing.  The KV cache of one call is
 132 MiB, which fits the 256 MB MALL, so the timed loop rotates over --copies
@@ -90,7 +92,13 @@ def main():
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
 
-    def call(i):
+    counters = torch.zeros(kvh, dtype=torch.int32, device=dev)  # zeroed once; every call leaves them zero
+
+    def call(i):  # one decode-attention call: single launch, last work-group merges
+        kvb.decode_attention_fused(s, inps[i % len(inps)], st, scratch, counters, m, l, n, out, kvb.KVB_OUT_F16,
+                                   sp)
+
+    def call_two_launch(i):  # split kernel + merge kernel
         kvb.decode_attention(s, inps[i % len(inps)], st, scratch, m, l, n, out, kvb.KVB_OUT_F16, sp)
 
     # ---- parity of the benchmarked configuration against the FP64 oracle.
@@ -127,6 +135,12 @@ def main():
     e1.record(stream)
     torch.cuda.synchronize()
     eager_ms = e0.elapsed_time(e1) / args.steps
+    e0.record(stream)
+    for i in range(args.steps):
+        call_two_launch(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    two_launch_ms = e0.elapsed_time(e1) / args.steps
 
     # ---- hipGraph replay: one graph holds one call per KV copy
     graph_ms = None
@@ -139,7 +153,8 @@ def main():
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=gs):
             for c in range(len(inps)):
-                kvb.decode_attention(s, inps[c], st, scratch, m, l, n, out, kvb.KVB_OUT_F16, gs.cuda_stream)
+                kvb.decode_attention_fused(s, inps[c], st, scratch, counters, m, l, n, out, kvb.KVB_OUT_F16,
+                                           gs.cuda_stream)
         torch.cuda.synchronize()
         reps = max(1, args.steps // len(inps))
         for _ in range(3):
@@ -182,6 +197,7 @@ def main():
     call_ms = graph_ms if graph_ms is not None else eager_ms
     value = kv_bytes / (call_ms * 1e-3) / 1e9
     split_gbs = kv_bytes / (split_ms * 1e-3) / 1e9
+    log(f"two-launch eager {two_launch_ms*1e3:.2f} us/call")
     log(f"eager {eager_ms*1e3:.2f} us/call, graph {graph_ms*1e3 if graph_ms else float('nan'):.2f} us/call, "
         f"{split_kernel} {split_ms*1e3:.2f} us/launch ({split_gbs:.0f} GB/s), merge-only {merge_ms*1e3:.2f} us")
 
@@ -236,6 +252,7 @@ def main():
         "us_per_call": round(call_ms * 1e3, 3),
         "pct_of_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "eager_us_per_call": round(eager_ms * 1e3, 3),
+        "two_launch_eager_us_per_call": round(two_launch_ms * 1e3, 3),
         "graph_us_per_call": round(graph_ms * 1e3, 3) if graph_ms is not None else None,
         "split_kernel_us": round(split_ms * 1e3, 3),
         "merge_kernel_us": round(merge_ms * 1e3, 3),

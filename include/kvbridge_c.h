@@ -102,6 +102,19 @@ int kvb_merge_finalize(const kvb_shape* s, const float* scratch, uint32_t splits
 int kvb_decode_attention(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens,
                          float* scratch, float* m, float* l, float* n, void* out, int out_type,
                          void* stream);
+/* Extension (no counterpart in the reference library; for decode loops that
+ * want one launch per call): kvb_decode_attention as a single kernel where
+ * the int8-MFMA split kernel serves the shape -- the last work-group to finish
+ * for each kv head merges that head's splits (log-sum-exp, split order) into
+ * m, l, n and out.  Otherwise it runs the two launches of
+ * kvb_decode_attention.  `counters` holds kv_heads uint32 that must be zero
+ * before the first call; every call leaves them zero (allocate and zero them
+ * once, e.g. next to the scratch buffer).  Calls sharing `counters` must not
+ * overlap in time (same rule as for scratch).  m, l, n, out equal those of
+ * kvb_decode_attention up to fp32 summation order in the merge. */
+int kvb_decode_attention_fused(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens,
+                               float* scratch, uint32_t* counters, float* m, float* l, float* n, void* out,
+                               int out_type, void* stream);
 /* Extension (diagnostic): which split kernel kvb_split_attention would run for
  * these arguments: KVB_KERNEL_TILED_MFMA or KVB_KERNEL_GENERIC; 0 if invalid. */
 int kvb_selected_kernel(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens);

@@ -148,6 +148,15 @@ def decode_attention(s: Shape, inp: DeviceInput, split_tokens: int, scratch, m, 
                                       _ptr(n), _ptr(out), out_type, _stream(stream)))
 
 
+def decode_attention_fused(s: Shape, inp: DeviceInput, split_tokens: int, scratch, counters, m, l, n, out=None,
+                           out_type: int = KVB_OUT_NONE, stream=None) -> None:
+    """Single-launch decode (kvb_decode_attention_fused): `counters` is a
+    device uint32 buffer of kv_heads zeros, left zero by every call."""
+    check(load().kvb_decode_attention_fused(ctypes.byref(s), ctypes.byref(inp), split_tokens, _ptr(scratch),
+                                            _ptr(counters), _ptr(m), _ptr(l), _ptr(n), _ptr(out), out_type,
+                                            _stream(stream)))
+
+
 def selected_kernel(s: Shape, inp: DeviceInput, split_tokens: int) -> int:
     return load().kvb_selected_kernel(ctypes.byref(s), ctypes.byref(inp), split_tokens)
 

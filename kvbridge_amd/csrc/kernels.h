@@ -22,6 +22,16 @@ struct SplitArgs {
   uint32_t rows, q_heads, kv_heads, group, dim, page_tokens, pages, begin, end;
   uint32_t split_tokens, splits;
   float scale;
+  // Fused merge (kvb_decode_attention_fused): non-null counters make the
+  // last work-group of each kv head merge that head's splits into m, l, n
+  // (and out when out_type != 0).  counters[kv_heads] must be zero on entry
+  // and are zero again when the kernel ends.
+  uint32_t* counters;
+  float* m;
+  float* l;
+  float* n;
+  void* out;
+  int out_type;
 };
 
 SplitArgs make_split_args(const kvbridge::Shape& s, const kvbridge::DeviceInput& in,
@@ -33,6 +43,7 @@ bool tiled_supported(const kvbridge::Shape& s, const kvbridge::DeviceInput& in);
 hipError_t launch_split_lds(const SplitArgs& a, hipStream_t stream);  // LDS-DMA-staged tiles, f16 MFMA
 hipError_t launch_split_i8(const SplitArgs& a, hipStream_t stream);   // register-staged tiles, int8 MFMA
 bool i8_supported(const SplitArgs& a);  // head_rows <= 8 (<= 4 at dim 256), power-of-two pages
+bool i8_fusable(const SplitArgs& a);    // the int8 kernel can run the fused merge
 // The MFMA split path used by the entry points: the int8-MFMA kernel where
 // i8_supported, else the f16-MFMA LDS kernel.  KVB_SPLIT_IMPL=f16 forces the
 // f16 kernel (comparisons).

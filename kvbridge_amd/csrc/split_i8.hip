@@ -184,6 +184,86 @@ struct I8Layout {
   static constexpr uint32_t kBytes = NW * kWave > kCombine ? NW * kWave : kCombine;
 };
 
+// Merge of all splits of one kv head's head-rows, by the last work-group:
+// thread (head-row hh, dim d) reads m_j, l_j and n_j[d] of every split j and
+// applies the reference merge in split order (src/attention_shared.cu:
+// 295-335): M = max_j m_j; L = sum_{l_j > 0} e^{m_j - M} l_j; N[d] likewise;
+// an all-empty head-row gives M = -inf, L = 0, N = 0.  Optional normalized
+// output out = L > 0 ? N / L : 0 (fp32 or fp16).
+// Agent-scope (all XCDs) coherent load of a partial written by another
+// work-group with an agent-scope atomic store.
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int D, int NW>
+__device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uint32_t head_rows,
+                                            const float* __restrict__ scratch) {
+  constexpr uint32_t W = D + 2;
+  constexpr uint32_t C = 32;  // splits whose loads are in flight together
+  for (uint32_t idx = threadIdx.x; idx < head_rows * D; idx += 64u * NW) {
+    const uint32_t hh = idx / D, d = idx % D;
+    const uint32_t row = hh / a.group, head = kv * a.group + hh % a.group;
+    const size_t rh = size_t(row) * a.q_heads + head;
+    const float* base = scratch + rh * a.splits * W;
+    float mx = neg_inf();
+    float lsum = 0.f, nacc = 0.f;
+    if (a.splits <= C) {  // one round trip: every partial's m, l, n[d] in flight together
+      float mv[C], lv[C], nv[C];
+#pragma unroll
+      for (uint32_t c = 0; c < C; ++c) {
+        const bool in = c < a.splits;
+        const float* p = base + size_t(in ? c : 0u) * W;
+        mv[c] = in ? ld_agent(p) : neg_inf();
+        lv[c] = in ? ld_agent(p + 1) : 0.f;
+        nv[c] = in ? ld_agent(p + 2 + d) : 0.f;
+      }
+#pragma unroll
+      for (uint32_t c = 0; c < C; ++c) mx = fmaxf(mx, mv[c]);
+#pragma unroll
+      for (uint32_t c = 0; c < C; ++c) {
+        const float f = lv[c] > 0.f ? exp_e(mv[c] - mx) : 0.f;
+        lsum = fmaf(f, lv[c], lsum);
+        nacc = fmaf(f, nv[c], nacc);
+      }
+    }
+    for (uint32_t j0 = 0; a.splits > C && j0 < a.splits; j0 += C) {
+      float mv[C];
+#pragma unroll
+      for (uint32_t c = 0; c < C; ++c) mv[c] = j0 + c < a.splits ? ld_agent(base + size_t(j0 + c) * W) : neg_inf();
+#pragma unroll
+      for (uint32_t c = 0; c < C; ++c) mx = fmaxf(mx, mv[c]);
+    }
+    for (uint32_t j0 = 0; a.splits > C && j0 < a.splits; j0 += C) {
+      float mv[C], lv[C], nv[C];
+#pragma unroll
+      for (uint32_t c = 0; c < C; ++c) {
+        const bool in = j0 + c < a.splits;
+        const float* p = base + size_t(in ? j0 + c : 0u) * W;
+        mv[c] = in ? ld_agent(p) : 0.f;
+        lv[c] = in ? ld_agent(p + 1) : 0.f;
+        nv[c] = in ? ld_agent(p + 2 + d) : 0.f;
+      }
+#pragma unroll
+      for (uint32_t c = 0; c < C; ++c) {
+        const float f = lv[c] > 0.f ? exp_e(mv[c] - mx) : 0.f;
+        lsum = fmaf(f, lv[c], lsum);
+        nacc = fmaf(f, nv[c], nacc);
+      }
+    }
+    if (d == 0) {
+      a.m[rh] = mx;
+      a.l[rh] = lsum;
+    }
+    a.n[rh * D + d] = nacc;
+    if (a.out_type != 0) {
+      const float o = lsum > 0.f ? nacc / lsum : 0.f;
+      if (a.out_type == 1) static_cast<float*>(a.out)[rh * D + d] = o;
+      else static_cast<_Float16*>(a.out)[rh * D + d] = (_Float16)o;
+    }
+  }
+}
+
 template <int D, int NW, int NB, bool PT, int HS>
 __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
     SplitArgs a, const float* __restrict__ q, const int64_t* __restrict__ qpos,
@@ -241,6 +321,20 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
   // the MFMA-result hazards and lgkmcnt waits).
   uint8_t* const wbase = smem + wave * L::kWave;
 
+  // ---- Q of the work-group's head-rows, staged once in LDS (one element
+  // per thread, loaded ahead of the KV stream); every wave builds its MFMA
+  // digit columns from there while the first KV item is in flight.
+  __shared__ float q_s[HS * D];
+  for (uint32_t i = threadIdx.x; i < HS * D; i += 64u * NW) {
+    const uint32_t h = i / D, d = i % D;
+    float x = 0.f;
+    if (h < head_rows) {
+      const uint32_t row = h / a.group, head = kv * a.group + h % a.group;
+      x = q[(size_t(row) * a.q_heads + head) * D + d];
+    }
+    q_s[i] = x;
+  }
+
   // ---- visibility per head-row: tokens [s0, eh[h]) (k_positions nondecreasing)
   uint32_t eh[HS];
   {
@@ -295,6 +389,7 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
   static_for<0, NB - 1>([&](auto uc) __attribute__((always_inline)) { issue(uc, 0u, ring[decltype(uc)::value]); });
 
   // ---- Q digits (B operand of QK) and per-head score factors.
+  __syncthreads();  // q_s complete
   i32x4 qd[NC][D / 64];
   float cql[HS];
   {
@@ -305,14 +400,16 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
       const uint32_t dg = col / HS, h = col % HS;
       const bool valid = col < 3u * HS && h < head_rows;
       float qv[D / 4];
-      if (valid) {
-        const uint32_t row = h / a.group, head = kv * a.group + h % a.group;
-        const float* qp = q + (size_t(row) * a.q_heads + head) * D + g * (D / 4);
+      {
+        const float* src = q_s + (valid ? h : 0u) * D + g * (D / 4);
 #pragma unroll
-        for (int i = 0; i < D / 4; ++i) qv[i] = __builtin_nontemporal_load(qp + i);
-      } else {
-#pragma unroll
-        for (int i = 0; i < D / 4; ++i) qv[i] = 0.f;
+        for (int i = 0; i < D / 16; ++i) {
+          const float4 w = reinterpret_cast<const float4*>(src)[i];
+          qv[4 * i] = valid ? w.x : 0.f;
+          qv[4 * i + 1] = valid ? w.y : 0.f;
+          qv[4 * i + 2] = valid ? w.z : 0.f;
+          qv[4 * i + 3] = valid ? w.w : 0.f;
+        }
       }
       float amax = 0.f;
 #pragma unroll
@@ -584,7 +681,33 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
       }
     }
     const uint32_t row2 = hh / a.group, head2 = kv * a.group + hh % a.group;
-    scratch[((size_t(row2) * a.q_heads + head2) * a.splits + split) * W + col] = val;
+    float* dst = scratch + ((size_t(row2) * a.q_heads + head2) * a.splits + split) * W + col;
+    if (a.counters != nullptr)
+      __hip_atomic_store(dst, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // agent-coherent
+    else
+      *dst = val;
+  }
+
+  // ---- fused merge: the last work-group to finish for this kv head merges
+  // its splits (agent-scope release of every partial, then a ticket).
+  if (a.counters != nullptr) {
+    __shared__ uint32_t last_s;
+    // The partials were stored with agent-scope atomic stores (coherent
+    // across XCDs, no L2 write-back needed) and are read back with
+    // agent-scope atomic loads.  Every wave waits until its stores have
+    // completed, the work-group synchronizes, and only then takes a ticket,
+    // so the work-group that draws the last ticket sees every partial.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t t = __hip_atomic_fetch_add(a.counters + kv, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_s = t + 1u == a.splits ? 1u : 0u;
+    }
+    __syncthreads();
+    if (last_s != 0u) {
+      fused_merge<D, NW>(a, kv, head_rows, scratch);
+      if (threadIdx.x == 0) __hip_atomic_store(a.counters + kv, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -602,45 +725,57 @@ hipError_t launch_i8(const SplitArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int D, int NW, int HS>
+template <int D, int NW, int NB, int HS>
 hipError_t preload_hs() {
   hipFuncAttributes attr{};
-  hipError_t e = hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_i8_kernel<D, NW, 2, true, HS>));
+  hipError_t e = hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS>));
   if (e != hipSuccess) return e;
-  return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_i8_kernel<D, NW, 2, false, HS>));
+  return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, false, HS>));
 }
 
-// Waves per work-group by tiles per split; eight waves (two per SIMD, <= 256
-// registers each) only where the state fits (HS <= 4, dim <= 128).
-// KVB_I8_WAVES (2, 4, 8) overrides (tuning sweeps).
-int i8_waves(const SplitArgs& a) {
+// (waves, ring slots) per work-group as 10*NW + NB, by tiles per split.
+// KVB_I8_CFG="NW,NB" overrides (tuning sweeps; unknown pairs fall back).
+int i8_config(const SplitArgs& a) {
   static const int forced = [] {
-    const char* e = std::getenv("KVB_I8_WAVES");
-    return e ? std::atoi(e) : 0;
+    const char* e = std::getenv("KVB_I8_CFG");
+    if (!e) return 0;
+    return std::atoi(e) * 10 + std::atoi(e + 2);
   }();
   const uint32_t tiles = (a.split_tokens + kTileTokens - 1) / kTileTokens;
-  int nw = forced ? forced : (tiles >= 16 ? 8 : (tiles >= 4 ? 4 : 2));
-  nw = nw >= 8 ? 8 : (nw >= 4 ? 4 : 2);
   const bool small = a.rows * a.group <= 4;
-  if (nw == 8 && !(small && a.dim <= 128)) nw = 4;
-  return nw;
+  int cfg = forced;
+  if (small && a.dim <= 128) {
+    if (cfg != 82 && cfg != 42 && cfg != 44 && cfg != 48 && cfg != 22 && cfg != 24)
+      cfg = tiles >= 16 ? 82 : (tiles >= 4 ? 42 : 22);
+  } else {
+    if (cfg != 42 && cfg != 44 && cfg != 22 && cfg != 24) cfg = tiles >= 4 ? 42 : 22;
+  }
+  return cfg;
 }
 
 template <int D, int HS>
 hipError_t launch_hs(const SplitArgs& a, hipStream_t stream) {
-  constexpr int NB = 2;
-  const int nw = i8_waves(a);
-  if constexpr (HS <= 4 && D <= 128) {
-    if (nw == 8) return launch_i8<D, 8, NB, HS>(a, stream);
+  switch (i8_config(a)) {
+    case 82:
+      if constexpr (HS <= 4 && D <= 128) return launch_i8<D, 8, 2, HS>(a, stream);
+      break;
+    case 48:
+      if constexpr (HS <= 4 && D <= 128) return launch_i8<D, 4, 8, HS>(a, stream);
+      break;
+    case 44: return launch_i8<D, 4, 4, HS>(a, stream);
+    case 42: return launch_i8<D, 4, 2, HS>(a, stream);
+    case 24: return launch_i8<D, 2, 4, HS>(a, stream);
+    default: break;
   }
-  if (nw == 4) return launch_i8<D, 4, NB, HS>(a, stream);
-  return launch_i8<D, 2, NB, HS>(a, stream);
+  return launch_i8<D, 2, 2, HS>(a, stream);
 }
 
 }  // namespace
 
 // head_rows <= 8 (<= 4 at dim 256); page_tokens a power of two >= 16; the
 // small-page path addresses K/V with 32-bit offsets.
+bool i8_fusable(const SplitArgs& a) { return i8_supported(a); }
+
 bool i8_supported(const SplitArgs& a) {
   const uint32_t hr = a.rows * a.group, P = a.page_tokens;
   if (hr > 8 || (a.dim == 256 && hr > 4)) return false;
@@ -661,25 +796,32 @@ hipError_t launch_split_i8(const SplitArgs& a, hipStream_t stream) {
 
 const char* i8_kernel_name(const SplitArgs& a) {
   static thread_local char buf[96];
-  std::snprintf(buf, sizeof(buf), "split_i8_kernel<%u,%d,2,%s,%d>", a.dim, i8_waves(a),
+  const int cfg = i8_config(a);
+  std::snprintf(buf, sizeof(buf), "split_i8_kernel<%u,%d,%d,%s,%d>", a.dim, cfg / 10, cfg % 10,
                 a.page_tokens >= kTileTokens ? "true" : "false", a.rows * a.group <= 4 ? 4 : 8);
   return buf;
 }
 
+template <int D, int HS>
+hipError_t preload_d() {
+  hipError_t e;
+  if constexpr (HS <= 4 && D <= 128) {
+    if ((e = preload_hs<D, 8, 2, HS>()) != hipSuccess) return e;
+    if ((e = preload_hs<D, 4, 8, HS>()) != hipSuccess) return e;
+  }
+  if ((e = preload_hs<D, 4, 4, HS>()) != hipSuccess) return e;
+  if ((e = preload_hs<D, 4, 2, HS>()) != hipSuccess) return e;
+  if ((e = preload_hs<D, 2, 4, HS>()) != hipSuccess) return e;
+  return preload_hs<D, 2, 2, HS>();
+}
+
 hipError_t preload_i8() {
   hipError_t e;
-  if ((e = preload_hs<64, 8, 4>()) != hipSuccess) return e;
-  if ((e = preload_hs<64, 4, 4>()) != hipSuccess) return e;
-  if ((e = preload_hs<64, 2, 4>()) != hipSuccess) return e;
-  if ((e = preload_hs<64, 4, 8>()) != hipSuccess) return e;
-  if ((e = preload_hs<64, 2, 8>()) != hipSuccess) return e;
-  if ((e = preload_hs<128, 8, 4>()) != hipSuccess) return e;
-  if ((e = preload_hs<128, 4, 4>()) != hipSuccess) return e;
-  if ((e = preload_hs<128, 2, 4>()) != hipSuccess) return e;
-  if ((e = preload_hs<128, 4, 8>()) != hipSuccess) return e;
-  if ((e = preload_hs<128, 2, 8>()) != hipSuccess) return e;
-  if ((e = preload_hs<256, 4, 4>()) != hipSuccess) return e;
-  return preload_hs<256, 2, 4>();
+  if ((e = preload_d<64, 4>()) != hipSuccess) return e;
+  if ((e = preload_d<64, 8>()) != hipSuccess) return e;
+  if ((e = preload_d<128, 4>()) != hipSuccess) return e;
+  if ((e = preload_d<128, 8>()) != hipSuccess) return e;
+  return preload_d<256, 4>();
 }
 
 }  // namespace kvb
