@@ -119,9 +119,11 @@ int kvb_decode_attention_fused(const kvb_shape* s, const kvb_device_input* in, u
  * these arguments: KVB_KERNEL_TILED_MFMA or KVB_KERNEL_GENERIC; 0 if invalid. */
 int kvb_selected_kernel(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens);
 /* Extension (diagnostic): name of the kernel instance kvb_split_attention
- * would launch (as rocprofv3 reports it, e.g. "split_i8_kernel<128,8,2,true,4>");
- * "" if the arguments are invalid.  Points to thread-local or static storage. */
-const char* kvb_selected_kernel_name(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens);
+ * (fused = 0) or kvb_decode_attention_fused (fused != 0) would launch, as
+ * rocprofv3 reports it, e.g. "split_i8_kernel<128,8,2,true,4,false>"; "" if
+ * the arguments are invalid.  Points to thread-local or static storage. */
+const char* kvb_selected_kernel_name(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens,
+                                     int fused);
 
 /* Extension (diagnostic, no counterpart in the reference library): streams
  * `bytes` (a multiple of 16) of device memory with non-temporal 16-byte loads

@@ -161,8 +161,8 @@ def selected_kernel(s: Shape, inp: DeviceInput, split_tokens: int) -> int:
     return load().kvb_selected_kernel(ctypes.byref(s), ctypes.byref(inp), split_tokens)
 
 
-def selected_kernel_name(s: Shape, inp: DeviceInput, split_tokens: int) -> str:
-    return load().kvb_selected_kernel_name(ctypes.byref(s), ctypes.byref(inp), split_tokens).decode()
+def selected_kernel_name(s: Shape, inp: DeviceInput, split_tokens: int, fused: bool = False) -> str:
+    return load().kvb_selected_kernel_name(ctypes.byref(s), ctypes.byref(inp), split_tokens, int(fused)).decode()
 
 
 def hbm_read_probe(src, nbytes: int, sink, blocks: int, stream=None) -> None:

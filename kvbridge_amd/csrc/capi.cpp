@@ -390,7 +390,8 @@ int kvb_selected_kernel(const kvb_shape* sp, const kvb_device_input* ip, uint32_
   return kvb::tiled_supported(s, to_input(*ip)) ? KVB_KERNEL_TILED_MFMA : KVB_KERNEL_GENERIC;
 }
 
-const char* kvb_selected_kernel_name(const kvb_shape* sp, const kvb_device_input* ip, uint32_t split_tokens) {
+const char* kvb_selected_kernel_name(const kvb_shape* sp, const kvb_device_input* ip, uint32_t split_tokens,
+                                     int fused) {
   if (!sp || !ip || split_tokens == 0) return "";
   const kvbridge::Shape s = to_shape(*sp);
   if (!kvbridge::attention_shape_valid(s)) return "";
@@ -401,7 +402,9 @@ const char* kvb_selected_kernel_name(const kvb_shape* sp, const kvb_device_input
   } catch (...) {
     return "";
   }
-  const kvb::SplitArgs a = kvb::make_split_args(s, in, split_tokens, splits, nullptr);
+  kvb::SplitArgs a = kvb::make_split_args(s, in, split_tokens, splits, nullptr);
+  static uint32_t dummy_counter;  // only its non-nullness is read
+  if (fused && kvb::tiled_supported(s, in) && kvb::i8_fusable(a)) a.counters = &dummy_counter;
   return kvb::split_kernel_name(a, kvb::tiled_supported(s, in), s.int8);
 }
 

@@ -1,739 +1,27 @@
-// Integer-MFMA split-partial kernel for paged INT8 KV with few grouped
-// head-rows per KV head (head_rows = rows * q_heads/kv_heads <= 8).
-//
-// The INT8 codes are never converted: both contractions run on
-// v_mfma_i32_16x16x64_i8 with the raw K and V bytes as the A operand.
-//  * QK: Q of each head-row is scaled by a power of two to a 22-bit integer
-//    and split into three int8 digits (q = hi*2^16 + mid*2^8 + lo, exact).
-//    The digits of all head-rows sit side by side in the 16 MFMA columns
-//    (column = digit * HS + head), so one MFMA per 64 dims gives all three
-//    digit dot products for 16 tokens.
-//  * PV: the weights w * v_scale are scaled by 2^kp to integers below 2^20
-//    and split into three 7-bit digits (p = d0*2^14 + d1*2^7 + d2); the
-//    per-digit integer numerators accumulate exactly in int32.
-// Digit recombination and the softmax run in a transposed view where each
-// lane owns one token of the tile for every head-row (data moves through a
-// small per-wave LDS exchange area), so no VALU work is spent on padding
-// columns.
-//
-// Two passes per chunk of up to 4 tiles: the K images of the chunk are
-// streamed first (scores kept in registers, exact chunk maximum), then the V
-// images; the int32 numerators therefore never need an online rescale and
-// are folded into fp32 once per chunk.
-//
-// Staging: K and V bytes go from HBM straight into VGPRs, already in the
-// MFMA operand layout, with non-temporal 16-byte buffer loads (per-lane
-// constant voffset; the descriptor is rebased per tile on its page, so
-// every access is bounded by the page).  Each wave keeps a ring of NB item
-// slots in registers and issues item j+NB-1 before computing item j; items
-// run in fixed chunks (K images of 4 tiles, then their V images) so every
-// ring slot is a compile-time register set and the issue is unconditional
-// (an item past the wave's last tile gets a zero-sized descriptor and moves
-// no data), which lets the compiler's wait-count pass keep exact
-// per-register waits.  Eight waves per work-group (two per SIMD) where the
-// state fits in 256 registers.
-//
-// Partial layout and semantics are those of every split kernel here:
-// scratch[((row*q_heads + head)*splits + split)*(dim+2) + col], col 0 = split
-// max score (natural log units), 1 = sum of exp(score - max), 2.. =
-// sum of exp(score - max) * v_scale * v_code.
+// Host side of the integer-MFMA split kernel (split_i8.h): shape support,
+// the (waves, ring slots) choice, and dispatch to the per-dim translation
+// units split_i8_d64/_d128/_d256.hip (built in parallel).
 #include <cstdio>
 #include <cstdlib>
 
 #include "kernels.h"
-#include "device_common.h"
-#include "lds_stream.h"
 
 namespace kvb {
+
+hipError_t launch_i8_d64(const SplitArgs& a, int cfg, hipStream_t stream);
+hipError_t launch_i8_d128(const SplitArgs& a, int cfg, hipStream_t stream);
+hipError_t launch_i8_d256(const SplitArgs& a, int cfg, hipStream_t stream);
+hipError_t preload_i8_d64();
+hipError_t preload_i8_d128();
+hipError_t preload_i8_d256();
+
 namespace {
 
-using lds::static_for;
-using lds::u32x4_t;
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kTiles = 64;  // tokens per tile
 
-constexpr uint32_t kTileTokens = 64;
-constexpr int kChunk = 4;                    // tiles per two-pass chunk
-constexpr float kLn2 = 0.6931471805599453f;
-constexpr int32_t kRsrcWord3 = 0x00020000;   // raw 32-bit buffer, gfx9 dword3
-
-// ---- loads.  Compiler builtins, so that its wait-count pass tracks every
-// loaded register (in-order vmcnt; exact for this static schedule).
-constexpr int kAuxNT = 2;  // non-temporal
-__device__ __forceinline__ u32x4_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), int(soff), kAuxNT);
-}
-__device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, int(voff), int(soff), kAuxNT);
-}
-__device__ __forceinline__ u32x4_t gload16(const int8_t* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
-}
-__device__ __forceinline__ uint32_t gload4(const float* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
-}
-
-// One item in registers: the K image (d[mb * D/64 + j] = 16 bytes of K row
-// 16*(m/4) + 4*mb + m%4, dims 16*(g*D/64 + j) ..) or the V image (d[mb] = V row
-// 16*mb + m, slots 16g .. 16g+15), plus k- and v-scale of token lane.
-template <int D>
-struct Slot {
-  u32x4_t d[D / 16];
-  uint32_t ks, vs;
-};
-
-struct IssueCtx {
-  __amdgpu_buffer_rsrc_t rk, rv, rks, rvs;  // whole-array descriptors (small-page path)
-  uint32_t voff_k, voff_v, voff_s;          // per-lane constant offsets (page-tile path)
-  const int8_t* k;
-  const int8_t* v;
-  const float* ks;
-  const float* vs;
-  const uint32_t* table;
-  uint32_t kv, kv_heads, P, lg_p, pages, lp_lo, lp_hi, lane, ptab;
-  uint32_t kv_bytes, sc_bytes;  // small-page path: whole-array sizes (< 4 GiB)
-};
-
-typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
-
-// Physical page of logical page lp (uniform), clamped to the split's pages
-// and to the pool; the first 64 come from the wave's page-table window.
-__device__ __forceinline__ uint32_t page_of(const IssueCtx& c, uint32_t lp) {
-  lp = clampu(lp, c.lp_lo, c.lp_hi);
-  const uint32_t rel = lp - c.lp_lo;
-  uint32_t x = rel < 64u ? uint32_t(__builtin_amdgcn_readlane(int(c.ptab), int(rel)))
-                         : ((const_u32_ptr)(c.table))[lp];  // scalar load
-  x = uint32_t(__builtin_amdgcn_readfirstlane(int(x)));
-  return x < c.pages ? x : c.pages - 1u;
-}
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), kRsrcWord3);
-}
-
-// Issue one item (D/16 + 2 loads, unconditionally: an item past the wave's
-// last tile gets zero-sized descriptors, so its loads return 0 and move no
-// data).  PT: page_tokens is a power of two >= 64, the tile lies in one page
-// and the descriptors are rebased on it (any pool size).  Otherwise
-// page_tokens is 16 or 32: every 16-token group lies in one page and lanes
-// address their group's page through whole-array descriptors.
-template <int D, bool PT, bool IS_V>
-__device__ __forceinline__ void issue_item(const IssueCtx& c, uint32_t tile, bool real, Slot<D>& s) {
-  const uint32_t t0 = tile * kTileTokens;
-  if constexpr (PT) {
-    const uint64_t slab = page_of(c, t0 >> c.lg_p) * uint64_t(c.kv_heads) + c.kv;
-    const uint32_t slot0 = t0 & (c.P - 1u);
-    const uint64_t tok = slab * c.P + slot0;
-    if constexpr (!IS_V) {
-      const __amdgpu_buffer_rsrc_t r = rsrc(c.k + tok * D, real ? 64u * D : 0u);
-      static_for<0, 4>([&](auto mbc) __attribute__((always_inline)) {
-        constexpr uint32_t mb = decltype(mbc)::value;
-        static_for<0, D / 64>([&](auto jc) __attribute__((always_inline)) {
-          constexpr uint32_t j = decltype(jc)::value;
-          s.d[mb * (D / 64) + j] = bload16(r, c.voff_k + (4 * mb * D + 16 * j), 0u);
-        });
-      });
-    } else {
-      const __amdgpu_buffer_rsrc_t r = rsrc(c.v + slab * D * c.P + slot0, real ? D * c.P - slot0 : 0u);
-#pragma unroll
-      for (uint32_t mb = 0; mb < D / 16; ++mb) s.d[mb] = bload16(r, c.voff_v, 16u * mb * c.P);
-    }
-    s.ks = bload4(rsrc(c.ks + tok, real ? 256u : 0u), c.voff_s, 0u);
-    s.vs = bload4(rsrc(c.vs + tok, real ? 256u : 0u), c.voff_s, 0u);
-  } else {
-    const uint32_t lane = c.lane, m = lane & 15u, g = lane >> 4;
-    uint32_t slab[4];  // slab of token group q (tokens t0+16q ..), uniform
-#pragma unroll
-    for (uint32_t q = 0; q < 4; ++q) slab[q] = page_of(c, (t0 + 16u * q) >> c.lg_p) * c.kv_heads + c.kv;
-    auto pick = [&](uint32_t q) __attribute__((always_inline)) {
-      return q == 0 ? slab[0] : (q == 1 ? slab[1] : (q == 2 ? slab[2] : slab[3]));
-    };
-    const __amdgpu_buffer_rsrc_t none = rsrc(c.k, 0u);
-    if constexpr (!IS_V) {
-      const uint32_t grp = m >> 2;
-      const uint32_t row = pick(grp) * c.P + ((t0 + 16u * grp) & (c.P - 1u)) + (m & 3u);
-      const uint32_t voff = row * uint32_t(D) + 16u * (g * (D / 64));
-      const __amdgpu_buffer_rsrc_t r = real ? c.rk : none;
-      static_for<0, 4>([&](auto mbc) __attribute__((always_inline)) {
-        constexpr uint32_t mb = decltype(mbc)::value;
-        static_for<0, D / 64>([&](auto jc) __attribute__((always_inline)) {
-          constexpr uint32_t j = decltype(jc)::value;
-          s.d[mb * (D / 64) + j] = bload16(r, voff + (4 * mb * D + 16 * j), 0u);
-        });
-      });
-    } else {
-      const uint32_t voff = (pick(g) * uint32_t(D) + m) * c.P + ((t0 + 16u * g) & (c.P - 1u));
-      const __amdgpu_buffer_rsrc_t r = real ? c.rv : none;
-#pragma unroll
-      for (uint32_t mb = 0; mb < D / 16; ++mb) s.d[mb] = bload16(r, voff, 16u * mb * c.P);
-    }
-    const uint32_t si = (pick(g) * c.P + ((t0 + 16u * g) & (c.P - 1u)) + m) * 4u;
-    s.ks = bload4(real ? c.rks : none, si, 0u);
-    s.vs = bload4(real ? c.rvs : none, si, 0u);
-  }
-}
-
-template <int D, int NW, int HS>
-struct I8Layout {
-  static constexpr int NC = (3 * HS + 15) / 16;       // MFMA column tiles
-  static constexpr uint32_t kExchCol = 272;           // int32 column of 64 tokens + pad
-  static constexpr uint32_t kDigCol = 80;             // int8 column of 64 tokens + pad
-  static constexpr uint32_t kExch = NC * 16 * kExchCol;
-  static constexpr uint32_t kDig = NC * 16 * kDigCol;
-  static constexpr uint32_t kWave = kExch + kDig;
-  static constexpr uint32_t kCombine = NW * 16 * (D + 2) * 4;
-  static constexpr uint32_t kBytes = NW * kWave > kCombine ? NW * kWave : kCombine;
-};
-
-// Merge of all splits of one kv head's head-rows, by the last work-group:
-// thread (head-row hh, dim d) reads m_j, l_j and n_j[d] of every split j and
-// applies the reference merge in split order (src/attention_shared.cu:
-// 295-335): M = max_j m_j; L = sum_{l_j > 0} e^{m_j - M} l_j; N[d] likewise;
-// an all-empty head-row gives M = -inf, L = 0, N = 0.  Optional normalized
-// output out = L > 0 ? N / L : 0 (fp32 or fp16).
-// Agent-scope (all XCDs) coherent load of a partial written by another
-// work-group with an agent-scope atomic store.
-__device__ __forceinline__ float ld_agent(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-template <int D, int NW>
-__device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uint32_t head_rows,
-                                            const float* __restrict__ scratch) {
-  constexpr uint32_t W = D + 2;
-  constexpr uint32_t C = 32;  // splits whose loads are in flight together
-  for (uint32_t idx = threadIdx.x; idx < head_rows * D; idx += 64u * NW) {
-    const uint32_t hh = idx / D, d = idx % D;
-    const uint32_t row = hh / a.group, head = kv * a.group + hh % a.group;
-    const size_t rh = size_t(row) * a.q_heads + head;
-    const float* base = scratch + rh * a.splits * W;
-    float mx = neg_inf();
-    float lsum = 0.f, nacc = 0.f;
-    if (a.splits <= C) {  // one round trip: every partial's m, l, n[d] in flight together
-      float mv[C], lv[C], nv[C];
-#pragma unroll
-      for (uint32_t c = 0; c < C; ++c) {
-        const bool in = c < a.splits;
-        const float* p = base + size_t(in ? c : 0u) * W;
-        mv[c] = in ? ld_agent(p) : neg_inf();
-        lv[c] = in ? ld_agent(p + 1) : 0.f;
-        nv[c] = in ? ld_agent(p + 2 + d) : 0.f;
-      }
-#pragma unroll
-      for (uint32_t c = 0; c < C; ++c) mx = fmaxf(mx, mv[c]);
-#pragma unroll
-      for (uint32_t c = 0; c < C; ++c) {
-        const float f = lv[c] > 0.f ? exp_e(mv[c] - mx) : 0.f;
-        lsum = fmaf(f, lv[c], lsum);
-        nacc = fmaf(f, nv[c], nacc);
-      }
-    }
-    for (uint32_t j0 = 0; a.splits > C && j0 < a.splits; j0 += C) {
-      float mv[C];
-#pragma unroll
-      for (uint32_t c = 0; c < C; ++c) mv[c] = j0 + c < a.splits ? ld_agent(base + size_t(j0 + c) * W) : neg_inf();
-#pragma unroll
-      for (uint32_t c = 0; c < C; ++c) mx = fmaxf(mx, mv[c]);
-    }
-    for (uint32_t j0 = 0; a.splits > C && j0 < a.splits; j0 += C) {
-      float mv[C], lv[C], nv[C];
-#pragma unroll
-      for (uint32_t c = 0; c < C; ++c) {
-        const bool in = j0 + c < a.splits;
-        const float* p = base + size_t(in ? j0 + c : 0u) * W;
-        mv[c] = in ? ld_agent(p) : 0.f;
-        lv[c] = in ? ld_agent(p + 1) : 0.f;
-        nv[c] = in ? ld_agent(p + 2 + d) : 0.f;
-      }
-#pragma unroll
-      for (uint32_t c = 0; c < C; ++c) {
-        const float f = lv[c] > 0.f ? exp_e(mv[c] - mx) : 0.f;
-        lsum = fmaf(f, lv[c], lsum);
-        nacc = fmaf(f, nv[c], nacc);
-      }
-    }
-    if (d == 0) {
-      a.m[rh] = mx;
-      a.l[rh] = lsum;
-    }
-    a.n[rh * D + d] = nacc;
-    if (a.out_type != 0) {
-      const float o = lsum > 0.f ? nacc / lsum : 0.f;
-      if (a.out_type == 1) static_cast<float*>(a.out)[rh * D + d] = o;
-      else static_cast<_Float16*>(a.out)[rh * D + d] = (_Float16)o;
-    }
-  }
-}
-
-template <int D, int NW, int NB, bool PT, int HS>
-__global__ __launch_bounds__(64 * NW) void split_i8_kernel(
-    SplitArgs a, const float* __restrict__ q, const int64_t* __restrict__ qpos,
-    const int64_t* __restrict__ kpos, const uint32_t* __restrict__ table,
-    const int8_t* __restrict__ kdata, const int8_t* __restrict__ vdata,
-    const float* __restrict__ kscale, const float* __restrict__ vscale, float* __restrict__ scratch) {
-  using L = I8Layout<D, NW, HS>;
-  constexpr int NC = L::NC;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[L::kBytes];
-
-  const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t n = lane & 15u, g = lane >> 4;
-  const uint32_t split = blockIdx.x;
-  const uint32_t kv = blockIdx.y;
-  const uint32_t head_rows = a.rows * a.group;  // <= HS
-
-  const uint64_t s0_64 = uint64_t(a.begin) + uint64_t(split) * a.split_tokens;
-  const uint32_t s0 = s0_64 < a.end ? uint32_t(s0_64) : a.end;
-  const uint32_t s1 = uint64_t(s0) + a.split_tokens < a.end ? s0 + a.split_tokens : a.end;
-  const uint32_t k_first = s0 / kTileTokens;
-
-  IssueCtx c;
-  c.k = kdata;
-  c.v = vdata;
-  c.ks = kscale;
-  c.vs = vscale;
-  c.table = table;
-  c.kv = kv;
-  c.kv_heads = a.kv_heads;
-  c.P = a.page_tokens;
-  c.pages = a.pages;
-  c.lp_lo = s0 / a.page_tokens;
-  c.lp_hi = s1 > s0 ? (s1 - 1u) / a.page_tokens : c.lp_lo;
-  c.lane = lane;
-  c.lg_p = 31u - __builtin_clz(a.page_tokens);  // page_tokens is a power of two
-  {
-    const uint32_t lp = c.lp_lo + lane;
-    c.ptab = lp <= c.lp_hi ? table[lp] : 0u;
-  }
-  if constexpr (PT) {
-    c.voff_k = (16u * (n >> 2) + (n & 3u)) * uint32_t(D) + 16u * (g * (D / 64));
-    c.voff_v = n * a.page_tokens + 16u * g;
-    c.voff_s = 4u * lane;
-  } else {
-    const uint32_t kv_bytes = a.pages * a.kv_heads * a.page_tokens * uint32_t(D);  // < 4 GiB (host check)
-    const uint32_t sc_bytes = a.pages * a.kv_heads * a.page_tokens * 4u;
-    c.rk = rsrc(kdata, kv_bytes);
-    c.rv = rsrc(vdata, kv_bytes);
-    c.rks = rsrc(kscale, sc_bytes);
-    c.rvs = rsrc(vscale, sc_bytes);
-  }
-
-  // Per-wave LDS exchange areas (plain LDS accesses: the compiler inserts
-  // the MFMA-result hazards and lgkmcnt waits).
-  uint8_t* const wbase = smem + wave * L::kWave;
-
-  // ---- Q of the work-group's head-rows, staged once in LDS (one element
-  // per thread, loaded ahead of the KV stream); every wave builds its MFMA
-  // digit columns from there while the first KV item is in flight.
-  __shared__ float q_s[HS * D];
-  for (uint32_t i = threadIdx.x; i < HS * D; i += 64u * NW) {
-    const uint32_t h = i / D, d = i % D;
-    float x = 0.f;
-    if (h < head_rows) {
-      const uint32_t row = h / a.group, head = kv * a.group + h % a.group;
-      x = q[(size_t(row) * a.q_heads + head) * D + d];
-    }
-    q_s[i] = x;
-  }
-
-  // ---- visibility per head-row: tokens [s0, eh[h]) (k_positions nondecreasing)
-  uint32_t eh[HS];
-  {
-    uint32_t erow[HS];
-#pragma unroll
-    for (int r = 0; r < HS; ++r) erow[r] = s0;
-    if (s1 > s0) {
-      const int64_t klast = kpos[s1 - 1u];
-      for (uint32_t r = 0; r < a.rows; ++r) {
-        const int64_t qp = qpos[r];
-        const uint32_t e = klast <= qp ? s1 : visible_end(kpos, s0, s1, qp, lane);
-#pragma unroll
-        for (int rr = 0; rr < HS; ++rr)
-          if (uint32_t(rr) == r) erow[rr] = e;
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < HS; ++h) {
-      const uint32_t r = uint32_t(h) / a.group;
-      uint32_t e = s0;
-#pragma unroll
-      for (int rr = 0; rr < HS; ++rr)
-        if (uint32_t(rr) == r) e = erow[rr];
-      eh[h] = uint32_t(h) < head_rows ? __builtin_amdgcn_readfirstlane(e) : s0;
-    }
-  }
-  uint32_t e_min = 0xffffffffu, e_max = s0;
-#pragma unroll
-  for (int h = 0; h < HS; ++h) {
-    if (uint32_t(h) < head_rows) e_min = eh[h] < e_min ? eh[h] : e_min;
-    e_max = eh[h] > e_max ? eh[h] : e_max;
-  }
-
-  // ---- the wave's tiles (round-robin over the work-group).  Items run in
-  // chunks of 2*kChunk: K images of tiles 4c..4c+3, then their V images.
-  // Items of tiles past the wave's last tile load nothing (zero-sized
-  // descriptors); their stale slot contents are masked by tok_ok and zero
-  // weights.
-  const uint32_t k_vis = e_max > s0 ? (e_max - 1u) / kTileTokens : 0u;
-  const uint32_t k_count = e_max > s0 ? k_vis + 1u - k_first : 0u;
-  const uint32_t nt = k_count > wave ? (k_count - wave + NW - 1u) / NW : 0u;
-  const uint32_t n_chunks = (nt + kChunk - 1u) / kChunk;
-  auto tile_k = [&](uint32_t i) __attribute__((always_inline)) { return k_first + wave + i * NW; };
-  // Item at chunk position POS (0 .. 2*kChunk-1) of chunk ch.
-  auto issue = [&](auto posc, uint32_t ch, Slot<D>& slot) __attribute__((always_inline)) {
-    constexpr uint32_t pos = decltype(posc)::value;
-    const uint32_t i = ch * kChunk + pos % kChunk;
-    issue_item<D, PT, (pos >= uint32_t(kChunk))>(c, tile_k(i), i < nt, slot);
-  };
-  Slot<D> ring[NB];
-  // Start streaming before the Q set-up below.
-  static_for<0, NB - 1>([&](auto uc) __attribute__((always_inline)) { issue(uc, 0u, ring[decltype(uc)::value]); });
-
-  // ---- Q digits (B operand of QK) and per-head score factors.
-  __syncthreads();  // q_s complete
-  i32x4 qd[NC][D / 64];
-  float cql[HS];
-  {
-    int kq_lane = 0;
-#pragma unroll
-    for (int nc = 0; nc < NC; ++nc) {
-      const uint32_t col = 16u * nc + n;
-      const uint32_t dg = col / HS, h = col % HS;
-      const bool valid = col < 3u * HS && h < head_rows;
-      float qv[D / 4];
-      {
-        const float* src = q_s + (valid ? h : 0u) * D + g * (D / 4);
-#pragma unroll
-        for (int i = 0; i < D / 16; ++i) {
-          const float4 w = reinterpret_cast<const float4*>(src)[i];
-          qv[4 * i] = valid ? w.x : 0.f;
-          qv[4 * i + 1] = valid ? w.y : 0.f;
-          qv[4 * i + 2] = valid ? w.z : 0.f;
-          qv[4 * i + 3] = valid ? w.w : 0.f;
-        }
-      }
-      float amax = 0.f;
-#pragma unroll
-      for (int i = 0; i < D / 4; ++i) amax = fmaxf(amax, fabsf(qv[i]));
-      amax = rows_max(amax);
-      int kq = 0;
-      if (amax > 0.f) {
-        kq = 21 - __builtin_amdgcn_frexp_expf(amax);
-        kq = kq < -100 ? -100 : (kq > 100 ? 100 : kq);
-      }
-      if (nc == 0) kq_lane = kq;
-#pragma unroll
-      for (int s = 0; s < D / 64; ++s) {
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          uint32_t packed = 0;
-#pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            const int qi = int(__builtin_rintf(__builtin_amdgcn_ldexpf(qv[16 * s + 4 * j + b], kq)));
-            const int lo = int(int8_t(qi & 0xff));
-            const int r1 = (qi - lo) >> 8;
-            const int mid = int(int8_t(r1 & 0xff));
-            const int hi = (r1 - mid) >> 8;
-            const int d = dg == 0 ? hi : (dg == 1 ? mid : lo);
-            packed |= (uint32_t(d) & 0xffu) << (8 * b);
-          }
-          w[j] = valid ? packed : 0u;
-        }
-        qd[nc][s] = i32x4{int(w[0]), int(w[1]), int(w[2]), int(w[3])};
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < HS; ++h) {
-      const int kq = __builtin_amdgcn_readlane(kq_lane, h);
-      cql[h] = __builtin_amdgcn_ldexpf(a.scale, -kq) * kLog2e;
-    }
-  }
-
-  uint8_t* const exch_w = wbase + n * L::kExchCol + 64u * g;              // C write base (MFMA view)
-  const uint8_t* const exch_r = wbase + 4u * lane;                        // lane-as-token read base
-  uint8_t* const dig_w = wbase + L::kExch + lane;                         // digit write (lane-as-token)
-  const uint8_t* const dig_r = wbase + L::kExch + n * L::kDigCol + 16u * g;  // B operand read
-
-  // State.  Lane-as-token view: sc, mx, lw, lrun per head-row.  MFMA view:
-  // int32 digit numerators acc_i, fp32 numerators acc_f (head = lane & 15).
-  float sc[kChunk][HS];
-  float mx[HS], lw[HS], lrun[HS];
-  float m_run[HS], m_new[HS], mu[HS];
-  float vmx = 0.f;
-  int kp = 0;
-  i32x4 acc_i[NC][D / 16];
-  f32x4 acc_f[D / 16];
-#pragma unroll
-  for (int h = 0; h < HS; ++h) {
-    mx[h] = neg_inf();
-    lw[h] = 0.f;
-    lrun[h] = 0.f;
-    m_run[h] = neg_inf();
-    m_new[h] = neg_inf();
-    mu[h] = 0.f;
-#pragma unroll
-    for (int r = 0; r < kChunk; ++r) sc[r][h] = neg_inf();
-  }
-#pragma unroll
-  for (int mb = 0; mb < D / 16; ++mb) {
-    acc_f[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int nc = 0; nc < NC; ++nc) acc_i[nc][mb] = i32x4{0, 0, 0, 0};
-  }
-
-  // ---- pass 1 item: scores of chunk tile r (tile index i).
-  auto process_k = [&](auto rc, uint32_t i, const Slot<D>& it) __attribute__((always_inline)) {
-    constexpr uint32_t r = decltype(rc)::value;
-    const uint32_t t0 = tile_k(i) * kTileTokens;
-    const uint32_t tok = t0 + lane;
-    const bool real = i < nt;
-    const bool full = real && t0 >= s0 && t0 + kTileTokens <= e_min;
-    const bool tok_ok = full || (real && tok >= s0 && tok < e_max);
-    static_for<0, NC>([&](auto ncc) __attribute__((always_inline)) {
-      constexpr uint32_t nc = decltype(ncc)::value;
-      static_for<0, 4>([&](auto mbc) __attribute__((always_inline)) {
-        constexpr uint32_t mb = decltype(mbc)::value;
-        i32x4 cc = {0, 0, 0, 0};
-#pragma unroll
-        for (int s = 0; s < D / 64; ++s) {
-          const u32x4_t w = it.d[mb * (D / 64) + s];
-          const i32x4 av = {int(w[0]), int(w[1]), int(w[2]), int(w[3])};
-          cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, qd[nc][s], cc, 0, 0, 0);
-        }
-        const u32x4_t cw = {uint32_t(cc[0]), uint32_t(cc[1]), uint32_t(cc[2]), uint32_t(cc[3])};
-        *reinterpret_cast<u32x4_t*>(exch_w + (nc * 16 * L::kExchCol + 16 * mb)) = cw;
-      });
-    });
-    int dv[HS][3];
-    static_for<0, HS>([&](auto hc) __attribute__((always_inline)) {
-      constexpr uint32_t h = decltype(hc)::value;
-      static_for<0, 3>([&](auto dc) __attribute__((always_inline)) {
-        constexpr uint32_t dg = decltype(dc)::value;
-        constexpr uint32_t col = dg * HS + h;
-        dv[h][dg] = *reinterpret_cast<const int*>(exch_r + col * L::kExchCol);
-      });
-    });
-    const float ks_l = __uint_as_float(it.ks);
-    const float vs_l = __uint_as_float(it.vs);
-    vmx = fmaxf(vmx, tok_ok ? fabsf(vs_l) : 0.f);
-#pragma unroll
-    for (int h = 0; h < HS; ++h) {
-      const float si = fmaf(fmaf(float(dv[h][0]), 256.f, float(dv[h][1])), 256.f, float(dv[h][2]));
-      float s2 = si * (ks_l * cql[h]);
-      if (!full && !(real && tok >= s0 && tok < eh[h])) s2 = neg_inf();
-      if (uint32_t(h) >= head_rows) s2 = neg_inf();
-      sc[r][h] = s2;
-      mx[h] = fmaxf(mx[h], s2);
-    }
-  };
-
-  // ---- pass 2 item: weights of chunk tile r, PV.
-  auto process_v = [&](auto rc, uint32_t i, const Slot<D>& it) __attribute__((always_inline)) {
-    constexpr uint32_t r = decltype(rc)::value;
-    const uint32_t t0 = tile_k(i) * kTileTokens;
-    const uint32_t tok = t0 + lane;
-    const bool real = i < nt;
-    const bool tok_ok = real && ((t0 >= s0 && t0 + kTileTokens <= e_min) || (tok >= s0 && tok < e_max));
-    const float vs_l = tok_ok ? __uint_as_float(it.vs) : 0.f;
-    static_for<0, HS>([&](auto hc) __attribute__((always_inline)) {
-      constexpr uint32_t h = decltype(hc)::value;
-      const float w = __builtin_amdgcn_exp2f(sc[r][h] - mu[h]);  // w * 2^kp
-      lw[h] += w;
-      const int pint = int(__builtin_rintf(w * vs_l));
-      const uint32_t d0 = uint32_t(pint >> 14) & 0xffu;
-      const uint32_t d1 = (uint32_t(pint) >> 7) & 0x7fu;
-      const uint32_t d2 = uint32_t(pint) & 0x7fu;
-      dig_w[h * L::kDigCol] = uint8_t(d0);
-      dig_w[(HS + h) * L::kDigCol] = uint8_t(d1);
-      dig_w[(2 * HS + h) * L::kDigCol] = uint8_t(d2);
-    });
-    u32x4_t bd[NC];
-    static_for<0, NC>([&](auto ncc) __attribute__((always_inline)) {
-      constexpr uint32_t nc = decltype(ncc)::value;
-      bd[nc] = *reinterpret_cast<const u32x4_t*>(dig_r + nc * 16 * L::kDigCol);
-    });
-#pragma unroll
-    for (int nc = 0; nc < NC; ++nc) {
-      const i32x4 bv = {int(bd[nc][0]), int(bd[nc][1]), int(bd[nc][2]), int(bd[nc][3])};
-#pragma unroll
-      for (int mb = 0; mb < D / 16; ++mb) {
-        const u32x4_t w = it.d[mb];
-        const i32x4 av = {int(w[0]), int(w[1]), int(w[2]), int(w[3])};
-        acc_i[nc][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, acc_i[nc][mb], 0, 0, 0);
-      }
-    }
-  };
-
-  // ---- chunk maximum and weight exponent kp (after the chunk's K items).
-  auto chunk_max = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int h = 0; h < HS; ++h) {
-      const float mc = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_max(mx[h]))));
-      m_new[h] = fmaxf(m_run[h], mc);
-      mx[h] = neg_inf();
-    }
-    const float vmax = wave_max(vmx);
-    vmx = 0.f;
-    kp = 0;
-    if (vmax > 0.f) {
-      kp = 20 - __builtin_amdgcn_frexp_expf(vmax);
-      kp = kp < -100 ? -100 : (kp > 100 ? 100 : kp);
-    }
-#pragma unroll
-    for (int h = 0; h < HS; ++h) mu[h] = (m_new[h] == neg_inf() ? 0.f : m_new[h]) - float(kp);
-  };
-
-  // ---- fold the chunk's int32 digit numerators into the fp32 state.
-  auto fold = [&]() __attribute__((always_inline)) {
-    float fh[HS];
-#pragma unroll
-    for (int h = 0; h < HS; ++h) {
-      fh[h] = m_run[h] == neg_inf() ? 0.f : __builtin_amdgcn_exp2f(m_run[h] - m_new[h]);
-      lrun[h] = fmaf(lrun[h], fh[h], __builtin_amdgcn_ldexpf(lw[h], -kp));
-      lw[h] = 0.f;
-      m_run[h] = m_new[h];
-    }
-    float f_lane = 0.f;  // head (lane & 15) of the MFMA view
-#pragma unroll
-    for (int h = 0; h < HS; ++h)
-      if (n == uint32_t(h)) f_lane = fh[h];
-    const float inv = __builtin_amdgcn_ldexpf(1.f, -kp);
-#pragma unroll
-    for (int mb = 0; mb < D / 16; ++mb) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        // digit dg of head h is column dg*HS + h: tile (dg*HS+h)/16, lane shift (dg*HS)%16.
-        const float x0 = float(acc_i[0][mb][e]);
-        float x1, x2;
-        if constexpr (HS <= 5) {
-          x1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x0), 0x100 + HS, 0xF, 0xF, true));
-          x2 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x0), 0x100 + 2 * HS, 0xF, 0xF, true));
-        } else {
-          x1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x0), 0x100 + (HS % 16), 0xF, 0xF, true));
-          x2 = float(acc_i[NC - 1][mb][e]);  // column 2*HS + h = 16 + h for HS == 8
-        }
-        const float comb = fmaf(fmaf(x0, 128.f, x1), 128.f, x2);
-        acc_f[mb][e] = fmaf(acc_f[mb][e], f_lane, comb * inv);
-      }
-#pragma unroll
-      for (int nc = 0; nc < NC; ++nc) acc_i[nc][mb] = i32x4{0, 0, 0, 0};
-    }
-  };
-
-  // ---- main loop: one chunk per iteration, items unrolled so that ring
-  // slots (item % NB, NB divides 2*kChunk) are compile-time.
-  static_assert((2 * kChunk) % NB == 0, "ring size must divide the chunk");
-  for (uint32_t ch = 0; ch < n_chunks; ++ch) {
-    static_for<0, 2 * kChunk>([&](auto uc) __attribute__((always_inline)) {
-      constexpr uint32_t u = decltype(uc)::value;
-      issue(std::integral_constant<uint32_t, (u + NB - 1) % (2 * kChunk)>(), ch + (u + NB - 1) / (2 * kChunk),
-            ring[(u + NB - 1) % NB]);
-      if constexpr (u < uint32_t(kChunk)) {
-        process_k(std::integral_constant<uint32_t, u>(), ch * kChunk + u, ring[u % NB]);
-        if constexpr (u == uint32_t(kChunk) - 1) chunk_max();
-      } else {
-        process_v(std::integral_constant<uint32_t, u - kChunk>(), ch * kChunk + (u - kChunk), ring[u % NB]);
-        if constexpr (u == 2u * kChunk - 1) fold();
-      }
-    });
-  }
-
-  // ---- combine the waves through LDS and write the split partial.
-  __syncthreads();
-  float* wm_s = reinterpret_cast<float*>(smem);   // [NW][16]
-  float* wl_s = wm_s + NW * 16;                   // [NW][16]
-  float* wacc_s = wl_s + NW * 16;                 // [NW][16][D]
-#pragma unroll
-  for (int h = 0; h < HS; ++h) {
-    const float lsum = wave_sum(lrun[h]);
-    if (lane == 0) {
-      wm_s[wave * 16 + h] = m_run[h] * kLn2;
-      wl_s[wave * 16 + h] = lsum;
-    }
-  }
-  if (n < uint32_t(HS)) {
-#pragma unroll
-    for (int mb = 0; mb < D / 16; ++mb) {
-      float4 y;
-      y.x = acc_f[mb][0];
-      y.y = acc_f[mb][1];
-      y.z = acc_f[mb][2];
-      y.w = acc_f[mb][3];
-      *reinterpret_cast<float4*>(&wacc_s[(wave * 16 + n) * D + 16 * mb + 4 * g]) = y;
-    }
-  }
-  __syncthreads();
-  constexpr uint32_t W = D + 2;
-  for (uint32_t idx = threadIdx.x; idx < head_rows * W; idx += 64u * NW) {
-    const uint32_t hh = idx / W, col = idx % W;
-    float mm = wm_s[hh];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) mm = fmaxf(mm, wm_s[w * 16 + hh]);
-    float val = mm;
-    if (col > 0) {
-      val = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        const float mw = wm_s[w * 16 + hh];
-        if (mw == neg_inf()) continue;
-        const float f = exp_e(mw - mm);
-        val = fmaf(f, col == 1 ? wl_s[w * 16 + hh] : wacc_s[(w * 16 + hh) * D + col - 2], val);
-      }
-    }
-    const uint32_t row2 = hh / a.group, head2 = kv * a.group + hh % a.group;
-    float* dst = scratch + ((size_t(row2) * a.q_heads + head2) * a.splits + split) * W + col;
-    if (a.counters != nullptr)
-      __hip_atomic_store(dst, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // agent-coherent
-    else
-      *dst = val;
-  }
-
-  // ---- fused merge: the last work-group to finish for this kv head merges
-  // its splits (agent-scope release of every partial, then a ticket).
-  if (a.counters != nullptr) {
-    __shared__ uint32_t last_s;
-    // The partials were stored with agent-scope atomic stores (coherent
-    // across XCDs, no L2 write-back needed) and are read back with
-    // agent-scope atomic loads.  Every wave waits until its stores have
-    // completed, the work-group synchronizes, and only then takes a ticket,
-    // so the work-group that draws the last ticket sees every partial.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const uint32_t t = __hip_atomic_fetch_add(a.counters + kv, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last_s = t + 1u == a.splits ? 1u : 0u;
-    }
-    __syncthreads();
-    if (last_s != 0u) {
-      fused_merge<D, NW>(a, kv, head_rows, scratch);
-      if (threadIdx.x == 0) __hip_atomic_store(a.counters + kv, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-}
-
-#define KVB_I8_ARGS                                                                              \
-  a, a.q, a.q_positions, a.k_positions, a.page_table, static_cast<const int8_t*>(a.k),             \
-      static_cast<const int8_t*>(a.v), a.k_scales, a.v_scales, a.scratch
-
-template <int D, int NW, int NB, int HS>
-hipError_t launch_i8(const SplitArgs& a, hipStream_t stream) {
-  const dim3 grid(a.splits, a.kv_heads);
-  if (a.page_tokens >= kTileTokens)
-    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, true, HS>), grid, dim3(64 * NW), 0, stream, KVB_I8_ARGS);
-  else
-    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, false, HS>), grid, dim3(64 * NW), 0, stream, KVB_I8_ARGS);
-  return hipGetLastError();
-}
-
-template <int D, int NW, int NB, int HS>
-hipError_t preload_hs() {
-  hipFuncAttributes attr{};
-  hipError_t e = hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS>));
-  if (e != hipSuccess) return e;
-  return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, false, HS>));
-}
-
-// (waves, ring slots) per work-group as 10*NW + NB, by tiles per split.
+// (waves, ring slots) per work-group as 10 * NW + NB, by tiles per split:
+// eight waves (two per SIMD, <= 256 registers each) where the state fits
+// (head_rows <= 4, dim <= 128) and the split has >= 16 tiles.
 // KVB_I8_CFG="NW,NB" overrides (tuning sweeps; unknown pairs fall back).
 int i8_config(const SplitArgs& a) {
   static const int forced = [] {
@@ -741,87 +29,52 @@ int i8_config(const SplitArgs& a) {
     if (!e) return 0;
     return std::atoi(e) * 10 + std::atoi(e + 2);
   }();
-  const uint32_t tiles = (a.split_tokens + kTileTokens - 1) / kTileTokens;
-  const bool small = a.rows * a.group <= 4;
-  int cfg = forced;
-  if (small && a.dim <= 128) {
-    if (cfg != 82 && cfg != 42 && cfg != 44 && cfg != 48 && cfg != 22 && cfg != 24)
-      cfg = tiles >= 16 ? 82 : (tiles >= 4 ? 42 : 22);
-  } else {
-    if (cfg != 42 && cfg != 44 && cfg != 22 && cfg != 24) cfg = tiles >= 4 ? 42 : 22;
-  }
-  return cfg;
-}
-
-template <int D, int HS>
-hipError_t launch_hs(const SplitArgs& a, hipStream_t stream) {
-  switch (i8_config(a)) {
-    case 82:
-      if constexpr (HS <= 4 && D <= 128) return launch_i8<D, 8, 2, HS>(a, stream);
-      break;
-    case 48:
-      if constexpr (HS <= 4 && D <= 128) return launch_i8<D, 4, 8, HS>(a, stream);
-      break;
-    case 44: return launch_i8<D, 4, 4, HS>(a, stream);
-    case 42: return launch_i8<D, 4, 2, HS>(a, stream);
-    case 24: return launch_i8<D, 2, 4, HS>(a, stream);
-    default: break;
-  }
-  return launch_i8<D, 2, 2, HS>(a, stream);
+  const uint32_t tiles = (a.split_tokens + kTiles - 1) / kTiles;
+  const bool eight = a.rows * a.group <= 4 && a.dim <= 128;
+  if (forced == 42 || forced == 22 || (forced == 82 && eight)) return forced;
+  if (eight && tiles >= 16) return 82;
+  return tiles >= 4 ? 42 : 22;
 }
 
 }  // namespace
 
 // head_rows <= 8 (<= 4 at dim 256); page_tokens a power of two >= 16; the
 // small-page path addresses K/V with 32-bit offsets.
-bool i8_fusable(const SplitArgs& a) { return i8_supported(a); }
-
 bool i8_supported(const SplitArgs& a) {
   const uint32_t hr = a.rows * a.group, P = a.page_tokens;
   if (hr > 8 || (a.dim == 256 && hr > 4)) return false;
+  if (a.dim != 64 && a.dim != 128 && a.dim != 256) return false;
   if (P < 16 || (P & (P - 1u)) != 0) return false;
-  if (P < kTileTokens && uint64_t(a.pages) * a.kv_heads * P * a.dim >= (uint64_t(1) << 32)) return false;
+  if (P < kTiles && uint64_t(a.pages) * a.kv_heads * P * a.dim >= (uint64_t(1) << 32)) return false;
   return true;
 }
 
+bool i8_fusable(const SplitArgs& a) { return i8_supported(a); }
+
 hipError_t launch_split_i8(const SplitArgs& a, hipStream_t stream) {
-  const bool small = a.rows * a.group <= 4;
+  const int cfg = i8_config(a);
   switch (a.dim) {
-    case 64: return small ? launch_hs<64, 4>(a, stream) : launch_hs<64, 8>(a, stream);
-    case 128: return small ? launch_hs<128, 4>(a, stream) : launch_hs<128, 8>(a, stream);
-    case 256: return launch_hs<256, 4>(a, stream);
+    case 64: return launch_i8_d64(a, cfg, stream);
+    case 128: return launch_i8_d128(a, cfg, stream);
+    case 256: return launch_i8_d256(a, cfg, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
 const char* i8_kernel_name(const SplitArgs& a) {
-  static thread_local char buf[96];
+  static thread_local char buf[112];
   const int cfg = i8_config(a);
-  std::snprintf(buf, sizeof(buf), "split_i8_kernel<%u,%d,%d,%s,%d>", a.dim, cfg / 10, cfg % 10,
-                a.page_tokens >= kTileTokens ? "true" : "false", a.rows * a.group <= 4 ? 4 : 8);
+  std::snprintf(buf, sizeof(buf), "split_i8_kernel<%u,%d,%d,%s,%d,%s>", a.dim, cfg / 10, cfg % 10,
+                a.page_tokens >= kTiles ? "true" : "false", a.rows * a.group <= 4 ? 4 : 8,
+                a.counters != nullptr ? "true" : "false");
   return buf;
 }
 
-template <int D, int HS>
-hipError_t preload_d() {
-  hipError_t e;
-  if constexpr (HS <= 4 && D <= 128) {
-    if ((e = preload_hs<D, 8, 2, HS>()) != hipSuccess) return e;
-    if ((e = preload_hs<D, 4, 8, HS>()) != hipSuccess) return e;
-  }
-  if ((e = preload_hs<D, 4, 4, HS>()) != hipSuccess) return e;
-  if ((e = preload_hs<D, 4, 2, HS>()) != hipSuccess) return e;
-  if ((e = preload_hs<D, 2, 4, HS>()) != hipSuccess) return e;
-  return preload_hs<D, 2, 2, HS>();
-}
-
 hipError_t preload_i8() {
-  hipError_t e;
-  if ((e = preload_d<64, 4>()) != hipSuccess) return e;
-  if ((e = preload_d<64, 8>()) != hipSuccess) return e;
-  if ((e = preload_d<128, 4>()) != hipSuccess) return e;
-  if ((e = preload_d<128, 8>()) != hipSuccess) return e;
-  return preload_d<256, 4>();
+  hipError_t e = preload_i8_d64();
+  if (e == hipSuccess) e = preload_i8_d128();
+  if (e == hipSuccess) e = preload_i8_d256();
+  return e;
 }
 
 }  // namespace kvb
