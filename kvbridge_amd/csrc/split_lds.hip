@@ -1,10 +1,14 @@
 // LDS-streamed MFMA split-partial kernel for paged INT8 KV (gfx950).
 //
-// Work decomposition, MFMA formulation and numerics are those of the tiled
-// kernel (split_tiled.hip): one work-group per (split, kv_head, block of <=16
-// head-rows); 64-token tiles; QK and PV as v_mfma_f32_16x16x32_f16 with the
-// KV tile as the A operand; f16 hi/lo Q and P; online softmax per wave; LDS
-// combine of the waves into the fp32 partial layout.
+// Used where the int8-MFMA kernel (split_i8.h) does not apply, notably more
+// than 8 head-rows per kv head (e.g. the reference's dense rows8/group6
+// geometry).  One work-group per (split, kv_head, block of <= 16 head-rows);
+// 64-token tiles split round-robin over the waves; QK and PV as
+// v_mfma_f32_16x16x32_f16 with the KV tile (int8 codes converted exactly to
+// f16) as the A operand and the head-rows as the 16 MFMA columns; Q and the
+// softmax weights P carried as f16 hi + lo pairs (scaled by powers of two)
+// so both products keep fp32-level accuracy; online softmax per wave and an
+// LDS combine of the waves into the fp32 partial layout.
 //
 // What differs is how a tile reaches the MFMA operands.  Each wave owns a
 // ring of NB tile buffers in LDS and fills them with gfx950's
@@ -290,7 +294,7 @@ __global__ __launch_bounds__(64 * NW) void split_lds_kernel(
   e_min = __builtin_amdgcn_readfirstlane(e_min);
   e_max = __builtin_amdgcn_readfirstlane(e_max);
 
-  // ---- Q (2^kq-scaled f16 hi/lo), exactly as in the tiled kernel.
+  // ---- Q as 2^kq-scaled f16 hi + lo (B operand of QK).
   float qv[D / 4];
   if (hvalid) {
     const float4* qp = reinterpret_cast<const float4*>(q + (size_t(row) * a.q_heads + head) * D + g * (D / 4));
