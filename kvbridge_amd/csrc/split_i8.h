@@ -184,83 +184,101 @@ struct I8Layout {
   static constexpr uint32_t kBytes = NW * kWave > kCombine ? NW * kWave : kCombine;
 };
 
-// Merge of all splits of one kv head's head-rows, by the last work-group:
-// thread (head-row hh, dim d) reads m_j, l_j and n_j[d] of every split j and
-// applies the reference merge in split order (src/attention_shared.cu:
-// 295-335): M = max_j m_j; L = sum_{l_j > 0} e^{m_j - M} l_j; N[d] likewise;
-// an all-empty head-row gives M = -inf, L = 0, N = 0.  Optional normalized
-// output out = L > 0 ? N / L : 0 (fp32 or fp16).
 // Agent-scope (all XCDs) coherent load of a partial written by another
 // work-group with an agent-scope atomic store.
 __device__ __forceinline__ float ld_agent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Merge of all splits of one kv head's head-rows, by the last work-group,
+// with the reference merge semantics (src/attention_shared.cu:295-335):
+// M = max_j m_j; L = sum_{l_j > 0} e^{m_j - M} l_j; N[d] likewise (fp32
+// sums in a fixed tree order rather than split order); an all-empty head-row
+// gives M = -inf, L = 0, N = 0.  Optional normalized output
+// out = L > 0 ? N / L : 0 (fp32 or fp16).  f_s: LDS [8][32], ml_s: LDS [8][2].
+
 template <int D, int NW>
 __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uint32_t head_rows,
-                                            const float* __restrict__ scratch) {
+                                            const float* __restrict__ scratch, float* f_s, float* ml_s) {
+  // Split factors: wave w takes head-rows w, w+NW, ...; lane j holds split
+  // j of the current chunk of 32: M = max m_j (over all splits), f_j =
+  // e^{m_j - M} (0 for l_j <= 0), L = sum f_j l_j; f_j go to LDS, M and L to
+  // ml_s.  Then
+  // thread (head-row, dim) sums f_j n_j[d].  When the splits fit one chunk
+  // and every thread owns one output, its n_j[d] loads are issued before the
+  // factor loads so both are in flight together (one memory round trip).
   constexpr uint32_t W = D + 2;
-  constexpr uint32_t C = 32;  // splits whose loads are in flight together
-  for (uint32_t idx = threadIdx.x; idx < head_rows * D; idx += 64u * NW) {
-    const uint32_t hh = idx / D, d = idx % D;
-    const uint32_t row = hh / a.group, head = kv * a.group + hh % a.group;
-    const size_t rh = size_t(row) * a.q_heads + head;
-    const float* base = scratch + rh * a.splits * W;
-    float mx = neg_inf();
-    float lsum = 0.f, nacc = 0.f;
-    if (a.splits <= C) {  // one round trip: every partial's m, l, n[d] in flight together
-      float mv[C], lv[C], nv[C];
+  constexpr uint32_t kCh = 32;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t outs = head_rows * D;
+  auto row_head = [&](uint32_t hh) __attribute__((always_inline)) {
+    return size_t(hh / a.group) * a.q_heads + kv * a.group + hh % a.group;
+  };
+  const bool one_pass = a.splits <= kCh && outs <= 64u * NW;
+  float pre[kCh];
+  if (one_pass && tid < outs) {
+    const float* base = scratch + row_head(tid / D) * a.splits * W + 2 + tid % D;
 #pragma unroll
-      for (uint32_t c = 0; c < C; ++c) {
-        const bool in = c < a.splits;
-        const float* p = base + size_t(in ? c : 0u) * W;
-        mv[c] = in ? ld_agent(p) : neg_inf();
-        lv[c] = in ? ld_agent(p + 1) : 0.f;
-        nv[c] = in ? ld_agent(p + 2 + d) : 0.f;
+    for (uint32_t j = 0; j < kCh; ++j) pre[j] = j < a.splits ? ld_agent(base + size_t(j) * W) : 0.f;
+  }
+  for (uint32_t j0 = 0; j0 < a.splits; j0 += kCh) {
+    const uint32_t cnt = a.splits - j0 < kCh ? a.splits - j0 : kCh;
+    for (uint32_t hh = wave; hh < head_rows; hh += NW) {
+      const float* base = scratch + row_head(hh) * a.splits * W;
+      float mx = neg_inf();
+      if (j0 == 0) {  // M over every split (chunks after the first reuse it)
+        for (uint32_t j = lane; j < a.splits; j += 64u) mx = fmaxf(mx, ld_agent(base + size_t(j) * W));
+        mx = wave_max(mx);
+      } else {
+        mx = ml_s[2 * hh];
       }
-#pragma unroll
-      for (uint32_t c = 0; c < C; ++c) mx = fmaxf(mx, mv[c]);
-#pragma unroll
-      for (uint32_t c = 0; c < C; ++c) {
-        const float f = lv[c] > 0.f ? exp_e(mv[c] - mx) : 0.f;
-        lsum = fmaf(f, lv[c], lsum);
-        nacc = fmaf(f, nv[c], nacc);
-      }
-    }
-    for (uint32_t j0 = 0; a.splits > C && j0 < a.splits; j0 += C) {
-      float mv[C];
-#pragma unroll
-      for (uint32_t c = 0; c < C; ++c) mv[c] = j0 + c < a.splits ? ld_agent(base + size_t(j0 + c) * W) : neg_inf();
-#pragma unroll
-      for (uint32_t c = 0; c < C; ++c) mx = fmaxf(mx, mv[c]);
-    }
-    for (uint32_t j0 = 0; a.splits > C && j0 < a.splits; j0 += C) {
-      float mv[C], lv[C], nv[C];
-#pragma unroll
-      for (uint32_t c = 0; c < C; ++c) {
-        const bool in = j0 + c < a.splits;
-        const float* p = base + size_t(in ? j0 + c : 0u) * W;
-        mv[c] = in ? ld_agent(p) : 0.f;
-        lv[c] = in ? ld_agent(p + 1) : 0.f;
-        nv[c] = in ? ld_agent(p + 2 + d) : 0.f;
-      }
-#pragma unroll
-      for (uint32_t c = 0; c < C; ++c) {
-        const float f = lv[c] > 0.f ? exp_e(mv[c] - mx) : 0.f;
-        lsum = fmaf(f, lv[c], lsum);
-        nacc = fmaf(f, nv[c], nacc);
+      const bool in = lane < cnt;  // lanes >= 32 idle
+      const float mj = in ? ld_agent(base + size_t(j0 + lane) * W) : neg_inf();
+      const float lj = in ? ld_agent(base + size_t(j0 + lane) * W + 1) : 0.f;
+      const float f = lj > 0.f ? exp_e(mj - mx) : 0.f;
+      const float lsum = wave_sum(f * lj);
+      if (lane < kCh) f_s[hh * kCh + lane] = f;
+      if (lane == 0) {
+        ml_s[2 * hh] = mx;
+        ml_s[2 * hh + 1] = (j0 == 0 ? 0.f : ml_s[2 * hh + 1]) + lsum;
       }
     }
-    if (d == 0) {
-      a.m[rh] = mx;
-      a.l[rh] = lsum;
+    __syncthreads();
+    for (uint32_t idx = tid; idx < outs; idx += 64u * NW) {
+      const uint32_t hh = idx / D, d = idx % D;
+      const float* fh = f_s + hh * kCh;
+      float nacc = 0.f;
+      if (one_pass) {
+#pragma unroll
+        for (uint32_t j = 0; j < kCh; ++j) nacc = fmaf(fh[j], pre[j], nacc);
+      } else {
+        const float* base = scratch + row_head(hh) * a.splits * W + 2 + d;
+        float nv[kCh];
+#pragma unroll
+        for (uint32_t j = 0; j < kCh; ++j) nv[j] = j < cnt ? ld_agent(base + size_t(j0 + j) * W) : 0.f;
+#pragma unroll
+        for (uint32_t j = 0; j < kCh; ++j) nacc = fmaf(fh[j], nv[j], nacc);
+        if (j0 != 0) nacc += a.n[row_head(hh) * D + d];
+      }
+      const bool last = j0 + kCh >= a.splits;
+      const size_t rh = row_head(hh);
+      if (!last) {
+        a.n[rh * D + d] = nacc;  // running numerator, re-read by this thread next chunk
+        continue;
+      }
+      const float lsum = ml_s[2 * hh + 1];
+      if (d == 0) {
+        a.m[rh] = ml_s[2 * hh];
+        a.l[rh] = lsum;
+      }
+      a.n[rh * D + d] = nacc;
+      if (a.out_type != 0) {
+        const float o = lsum > 0.f ? nacc / lsum : 0.f;
+        if (a.out_type == 1) static_cast<float*>(a.out)[rh * D + d] = o;
+        else static_cast<_Float16*>(a.out)[rh * D + d] = (_Float16)o;
+      }
     }
-    a.n[rh * D + d] = nacc;
-    if (a.out_type != 0) {
-      const float o = lsum > 0.f ? nacc / lsum : 0.f;
-      if (a.out_type == 1) static_cast<float*>(a.out)[rh * D + d] = o;
-      else static_cast<_Float16*>(a.out)[rh * D + d] = (_Float16)o;
-    }
+    __syncthreads();
   }
 }
 
@@ -705,7 +723,8 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
     }
     __syncthreads();
     if (last_s != 0u) {
-      fused_merge<D, NW>(a, kv, head_rows, scratch);
+      float* f_s = reinterpret_cast<float*>(smem);  // [HS][32] split factors
+      fused_merge<D, NW>(a, kv, head_rows, scratch, f_s, f_s + HS * 32);
       if (threadIdx.x == 0) __hip_atomic_store(a.counters + kv, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
@@ -751,6 +770,7 @@ hipError_t launch_dim(const SplitArgs& a, int cfg, hipStream_t stream) {
   if (a.rows * a.group <= 4) {
     if constexpr (D <= 128) {
       if (cfg == 82) return launch_cfg<D, 8, 2, 4>(a, stream);
+      if (cfg == 44) return launch_cfg<D, 4, 4, 4>(a, stream);
     }
     return cfg == 42 ? launch_cfg<D, 4, 2, 4>(a, stream) : launch_cfg<D, 2, 2, 4>(a, stream);
   }
@@ -763,6 +783,7 @@ hipError_t preload_dim() {
   hipError_t e = hipSuccess;
   if constexpr (D <= 128) {
     if (e == hipSuccess) e = preload_cfg<D, 8, 2, 4>();
+    if (e == hipSuccess) e = preload_cfg<D, 4, 4, 4>();
     if (e == hipSuccess) e = preload_cfg<D, 4, 2, 8>();
     if (e == hipSuccess) e = preload_cfg<D, 2, 2, 8>();
   }

@@ -31,7 +31,7 @@ int i8_config(const SplitArgs& a) {
   }();
   const uint32_t tiles = (a.split_tokens + kTiles - 1) / kTiles;
   const bool eight = a.rows * a.group <= 4 && a.dim <= 128;
-  if (forced == 42 || forced == 22 || (forced == 82 && eight)) return forced;
+  if (forced == 42 || forced == 22 || ((forced == 82 || forced == 44) && eight)) return forced;
   if (eight && tiles >= 16) return 82;
   return tiles >= 4 ? 42 : 22;
 }

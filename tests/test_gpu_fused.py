@@ -41,6 +41,9 @@ FUSED_SHAPES = [
     (1, 4, 4, 256, 64, 1111, 0, 1111, 512, None),       # dim 256
     (1, 8, 2, 64, 16, 300, 0, 300, 64, [-1]),           # every row-head empty
     (8, 48, 8, 128, 64, 640, 64, 640, 256, None),       # 48 head-rows: two-launch fallback
+    (1, 8, 2, 64, 16, 4096, 0, 4096, 64, None),         # 64 splits: merge in two chunks
+    (1, 32, 8, 128, 64, 8192, 5, 8192, 64, [6000]),     # 128 splits, causal cut, ragged begin
+    (2, 8, 2, 128, 32, 2000, 0, 2000, 32, [1999, 700]), # 8 head-rows, 63 splits
 ]
 
 
