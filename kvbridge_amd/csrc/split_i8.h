@@ -73,7 +73,7 @@ __device__ __forceinline__ uint32_t gload4(const float* p) {
 }
 
 // One item in registers: the K image (d[mb * D/64 + j] = 16 bytes of K row
-// 16*(m/4) + 4*mb + m%4, dims 16*(g*D/64 + j) ..) or the V image (d[mb] = V row
+// 16*(m/4) + 4*mb + m%4, dims 64*j + 16*g ..) or the V image (d[mb] = V row
 // 16*mb + m, slots 16g .. 16g+15), plus k- and v-scale of token lane.
 template <int D>
 struct Slot {
@@ -116,20 +116,27 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_
 // and the descriptors are rebased on it (any pool size).  Otherwise
 // page_tokens is 16 or 32: every 16-token group lies in one page and lanes
 // address their group's page through whole-array descriptors.
-template <int D, bool PT, bool IS_V>
+// PAIR (K image of the paired-row QK layout): MFMA row m of M-block mb is
+// half m%2 of token 8*mb + m/2, so the 16 lanes of a k-block read 8 rows x
+// 2 segments of one 128-byte line each instead of 16 rows.
+template <int D, bool PT, bool IS_V, bool PAIR>
 __device__ __forceinline__ void issue_item(const IssueCtx& c, uint32_t tile, bool real, Slot<D>& s) {
   const uint32_t t0 = tile * kTileTokens;
   if constexpr (PT) {
     const uint64_t slab = page_of(c, t0 >> c.lg_p) * uint64_t(c.kv_heads) + c.kv;
     const uint32_t slot0 = t0 & (c.P - 1u);
     const uint64_t tok = slab * c.P + slot0;
-    if constexpr (!IS_V) {
+    if constexpr (!IS_V && PAIR) {
+      const __amdgpu_buffer_rsrc_t r = rsrc(c.k + tok * D, real ? 64u * D : 0u);
+#pragma unroll
+      for (uint32_t mb = 0; mb < 8; ++mb) s.d[mb] = bload16(r, c.voff_k + 1024u * mb, 0u);
+    } else if constexpr (!IS_V) {
       const __amdgpu_buffer_rsrc_t r = rsrc(c.k + tok * D, real ? 64u * D : 0u);
       static_for<0, 4>([&](auto mbc) __attribute__((always_inline)) {
         constexpr uint32_t mb = decltype(mbc)::value;
         static_for<0, D / 64>([&](auto jc) __attribute__((always_inline)) {
           constexpr uint32_t j = decltype(jc)::value;
-          s.d[mb * (D / 64) + j] = bload16(r, c.voff_k + (4 * mb * D + 16 * j), 0u);
+          s.d[mb * (D / 64) + j] = bload16(r, c.voff_k + (4 * mb * D + 64 * j), 0u);
         });
       });
     } else {
@@ -148,16 +155,24 @@ __device__ __forceinline__ void issue_item(const IssueCtx& c, uint32_t tile, boo
       return q == 0 ? slab[0] : (q == 1 ? slab[1] : (q == 2 ? slab[2] : slab[3]));
     };
     const __amdgpu_buffer_rsrc_t none = rsrc(c.k, 0u);
-    if constexpr (!IS_V) {
+    if constexpr (!IS_V && PAIR) {
+      const __amdgpu_buffer_rsrc_t r = real ? c.rk : none;
+      static_for<0, 8>([&](auto mbc) __attribute__((always_inline)) {
+        constexpr uint32_t mb = decltype(mbc)::value;
+        constexpr uint32_t q = mb >> 1;  // 16-token group of tokens 8*mb ..
+        const uint32_t row = pick(q) * c.P + ((t0 + 16u * q) & (c.P - 1u)) + 8u * (mb & 1u) + (m >> 1);
+        s.d[mb] = bload16(r, row * uint32_t(D) + 64u * (m & 1u) + 16u * g, 0u);
+      });
+    } else if constexpr (!IS_V) {
       const uint32_t grp = m >> 2;
       const uint32_t row = pick(grp) * c.P + ((t0 + 16u * grp) & (c.P - 1u)) + (m & 3u);
-      const uint32_t voff = row * uint32_t(D) + 16u * (g * (D / 64));
+      const uint32_t voff = row * uint32_t(D) + 16u * g;
       const __amdgpu_buffer_rsrc_t r = real ? c.rk : none;
       static_for<0, 4>([&](auto mbc) __attribute__((always_inline)) {
         constexpr uint32_t mb = decltype(mbc)::value;
         static_for<0, D / 64>([&](auto jc) __attribute__((always_inline)) {
           constexpr uint32_t j = decltype(jc)::value;
-          s.d[mb * (D / 64) + j] = bload16(r, voff + (4 * mb * D + 16 * j), 0u);
+          s.d[mb * (D / 64) + j] = bload16(r, voff + (4 * mb * D + 64 * j), 0u);
         });
       });
     } else {
@@ -192,28 +207,23 @@ __device__ __forceinline__ float ld_agent(const float* p) {
 
 // Merge of all splits of one kv head's head-rows, by the last work-group,
 // with the reference merge semantics (src/attention_shared.cu:295-335):
-// M = max_j m_j; L = sum_{l_j > 0} e^{m_j - M} l_j; N[d] likewise (fp32
-// sums in a fixed tree order rather than split order); an all-empty head-row
-// gives M = -inf, L = 0, N = 0.  Optional normalized output
-// out = L > 0 ? N / L : 0 (fp32 or fp16).  f_s: LDS [8][32], ml_s: LDS [8][2].
-
+// M = max_j m_j; L = sum_{l_j > 0} e^{m_j - M} l_j; N[d] likewise (N summed
+// in split order, L by a wave tree); an all-empty head-row gives M = -inf,
+// L = 0, N = 0.  Optional normalized output out = L > 0 ? N / L : 0 (fp32 or
+// fp16).  f_s: LDS [8][32] split factors, ml_s: LDS [8][2] (M, L).
 template <int D, int NW>
 __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uint32_t head_rows,
                                             const float* __restrict__ scratch, float* f_s, float* ml_s) {
-  // Split factors: wave w takes head-rows w, w+NW, ...; lane j holds split
-  // j of the current chunk of 32: M = max m_j (over all splits), f_j =
-  // e^{m_j - M} (0 for l_j <= 0), L = sum f_j l_j; f_j go to LDS, M and L to
-  // ml_s.  Then
-  // thread (head-row, dim) sums f_j n_j[d].  When the splits fit one chunk
-  // and every thread owns one output, its n_j[d] loads are issued before the
-  // factor loads so both are in flight together (one memory round trip).
   constexpr uint32_t W = D + 2;
-  constexpr uint32_t kCh = 32;
+  constexpr uint32_t kCh = 32;  // splits per pass
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t outs = head_rows * D;
   auto row_head = [&](uint32_t hh) __attribute__((always_inline)) {
     return size_t(hh / a.group) * a.q_heads + kv * a.group + hh % a.group;
   };
+  // Common case (<= 32 splits, one output per thread): the thread's
+  // numerators and its wave's (m_j, l_j) are requested together, so the
+  // whole merge costs one memory round trip.
   const bool one_pass = a.splits <= kCh && outs <= 64u * NW;
   float pre[kCh];
   if (one_pass && tid < outs) {
@@ -225,16 +235,17 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
     const uint32_t cnt = a.splits - j0 < kCh ? a.splits - j0 : kCh;
     for (uint32_t hh = wave; hh < head_rows; hh += NW) {
       const float* base = scratch + row_head(hh) * a.splits * W;
-      float mx = neg_inf();
-      if (j0 == 0) {  // M over every split (chunks after the first reuse it)
-        for (uint32_t j = lane; j < a.splits; j += 64u) mx = fmaxf(mx, ld_agent(base + size_t(j) * W));
+      const bool in = lane < cnt;  // lanes >= 32 idle
+      const float mj = in ? ld_agent(base + size_t(j0 + lane) * W) : neg_inf();
+      const float lj = in ? ld_agent(base + size_t(j0 + lane) * W + 1) : 0.f;
+      float mx;
+      if (j0 == 0) {  // M over every split (later passes reuse it)
+        mx = mj;
+        for (uint32_t j = kCh + lane; j < a.splits; j += 64u) mx = fmaxf(mx, ld_agent(base + size_t(j) * W));
         mx = wave_max(mx);
       } else {
         mx = ml_s[2 * hh];
       }
-      const bool in = lane < cnt;  // lanes >= 32 idle
-      const float mj = in ? ld_agent(base + size_t(j0 + lane) * W) : neg_inf();
-      const float lj = in ? ld_agent(base + size_t(j0 + lane) * W + 1) : 0.f;
       const float f = lj > 0.f ? exp_e(mj - mx) : 0.f;
       const float lsum = wave_sum(f * lj);
       if (lane < kCh) f_s[hh * kCh + lane] = f;
@@ -247,23 +258,22 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
     for (uint32_t idx = tid; idx < outs; idx += 64u * NW) {
       const uint32_t hh = idx / D, d = idx % D;
       const float* fh = f_s + hh * kCh;
+      const size_t rh = row_head(hh);
       float nacc = 0.f;
       if (one_pass) {
 #pragma unroll
         for (uint32_t j = 0; j < kCh; ++j) nacc = fmaf(fh[j], pre[j], nacc);
       } else {
-        const float* base = scratch + row_head(hh) * a.splits * W + 2 + d;
+        const float* base = scratch + rh * a.splits * W + 2 + d;
         float nv[kCh];
 #pragma unroll
         for (uint32_t j = 0; j < kCh; ++j) nv[j] = j < cnt ? ld_agent(base + size_t(j0 + j) * W) : 0.f;
+        if (j0 != 0) nacc = a.n[rh * D + d];
 #pragma unroll
         for (uint32_t j = 0; j < kCh; ++j) nacc = fmaf(fh[j], nv[j], nacc);
-        if (j0 != 0) nacc += a.n[row_head(hh) * D + d];
       }
-      const bool last = j0 + kCh >= a.splits;
-      const size_t rh = row_head(hh);
-      if (!last) {
-        a.n[rh * D + d] = nacc;  // running numerator, re-read by this thread next chunk
+      if (j0 + kCh < a.splits) {
+        a.n[rh * D + d] = nacc;  // running numerator, re-read by this thread next pass
         continue;
       }
       const float lsum = ml_s[2 * hh + 1];
@@ -289,7 +299,15 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
     const int8_t* __restrict__ kdata, const int8_t* __restrict__ vdata,
     const float* __restrict__ kscale, const float* __restrict__ vscale, float* __restrict__ scratch) {
   using L = I8Layout<D, NW, HS>;
-  constexpr int NC = L::NC;
+  constexpr int NC = L::NC;  // MFMA column tiles of the digit columns (PV; QK unless PAIR)
+  // Paired-row QK (dim 128, <= 4 head-rows): MFMA row m of M-block mb is
+  // half m%2 (dims 64*(m%2) ..) of token 8*mb + m/2; column tile h of the Q
+  // digits holds half h, so rows and tiles of equal half give the two half
+  // dot products of a token, which add exactly in int32.  The K loads of a
+  // k-block then read whole 64-byte half rows, two per 128-byte line.
+  constexpr bool PAIR = D == 128 && HS <= 4;
+  constexpr int NCQ = PAIR ? 2 : NC;        // MFMA column tiles of the QK B operand
+  constexpr int KS = PAIR ? 1 : D / 64;     // 64-dim steps per QK M-block
   __shared__ __attribute__((aligned(16))) uint8_t smem[L::kBytes];
 
   const uint32_t lane = threadIdx.x & 63u;
@@ -323,7 +341,8 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
     c.ptab = lp <= c.lp_hi ? table[lp] : 0u;
   }
   if constexpr (PT) {
-    c.voff_k = (16u * (n >> 2) + (n & 3u)) * uint32_t(D) + 16u * (g * (D / 64));
+    c.voff_k = PAIR ? 128u * (n >> 1) + 64u * (n & 1u) + 16u * g
+                    : (16u * (n >> 2) + (n & 3u)) * uint32_t(D) + 16u * g;
     c.voff_v = n * a.page_tokens + 16u * g;
     c.voff_s = 4u * lane;
   } else {
@@ -339,18 +358,40 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
   // the MFMA-result hazards and lgkmcnt waits).
   uint8_t* const wbase = smem + wave * L::kWave;
 
-  // ---- Q of the work-group's head-rows, staged once in LDS (one element
-  // per thread, loaded ahead of the KV stream); every wave builds its MFMA
-  // digit columns from there while the first KV item is in flight.
-  __shared__ float q_s[HS * D];
-  for (uint32_t i = threadIdx.x; i < HS * D; i += 64u * NW) {
-    const uint32_t h = i / D, d = i % D;
-    float x = 0.f;
-    if (h < head_rows) {
-      const uint32_t row = h / a.group, head = kv * a.group + h % a.group;
-      x = q[(size_t(row) * a.q_heads + head) * D + d];
+  // ---- everything the KV stream and the Q digits depend on is loaded in
+  // one memory round trip: the page-table window (above), the split's last
+  // key position, the query positions, and the Q elements this lane turns
+  // into MFMA digit columns (straight into registers; no LDS staging and no
+  // work-group barrier before the stream starts).
+  const int64_t klast = s1 > s0 ? kpos[s1 - 1u] : 0;
+  int64_t qp[HS];
+#pragma unroll
+  for (int r = 0; r < HS; ++r) qp[r] = qpos[uint32_t(r) < a.rows ? uint32_t(r) : 0u];
+  // Lane (n, g) of MFMA column tile nc feeds a digit column: column
+  // 16*nc + n (digit dg = col / HS of head-row col % HS), or with PAIR column
+  // n of tile nc = half nc.  MFMA s of a 64-dim step takes dims 64*s + 16*g
+  // .. +15 of Q and K alike (PAIR: dims 64*nc + 16*g ..), so the K loads
+  // read whole 64-byte row segments.
+  float qv[NCQ][16 * KS];
+#pragma unroll
+  for (int nc = 0; nc < NCQ; ++nc) {
+    const uint32_t col = PAIR ? n : 16u * nc + n;
+    const uint32_t h = col % HS;
+    const bool valid = col < 3u * HS && h < head_rows;
+    const uint32_t hq = valid ? h : 0u;
+    const float* src = q + (size_t(hq / a.group) * a.q_heads + kv * a.group + hq % a.group) * D + 16u * g +
+                       (PAIR ? 64u * nc : 0u);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 w = reinterpret_cast<const float4*>(src + 64 * s)[j];
+        qv[nc][16 * s + 4 * j] = valid ? w.x : 0.f;
+        qv[nc][16 * s + 4 * j + 1] = valid ? w.y : 0.f;
+        qv[nc][16 * s + 4 * j + 2] = valid ? w.z : 0.f;
+        qv[nc][16 * s + 4 * j + 3] = valid ? w.w : 0.f;
+      }
     }
-    q_s[i] = x;
   }
 
   // ---- visibility per head-row: tokens [s0, eh[h]) (k_positions nondecreasing)
@@ -358,16 +399,10 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
   {
     uint32_t erow[HS];
 #pragma unroll
-    for (int r = 0; r < HS; ++r) erow[r] = s0;
-    if (s1 > s0) {
-      const int64_t klast = kpos[s1 - 1u];
-      for (uint32_t r = 0; r < a.rows; ++r) {
-        const int64_t qp = qpos[r];
-        const uint32_t e = klast <= qp ? s1 : visible_end(kpos, s0, s1, qp, lane);
-#pragma unroll
-        for (int rr = 0; rr < HS; ++rr)
-          if (uint32_t(rr) == r) erow[rr] = e;
-      }
+    for (int r = 0; r < HS; ++r) {
+      erow[r] = s0;
+      if (s1 > s0 && uint32_t(r) < a.rows)
+        erow[r] = klast <= qp[r] ? s1 : visible_end(kpos, s0, s1, qp[r], lane);
     }
 #pragma unroll
     for (int h = 0; h < HS; ++h) {
@@ -400,54 +435,59 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
   auto issue = [&](auto posc, uint32_t ch, Slot<D>& slot) __attribute__((always_inline)) {
     constexpr uint32_t pos = decltype(posc)::value;
     const uint32_t i = ch * kChunk + pos % kChunk;
-    issue_item<D, PT, (pos >= uint32_t(kChunk))>(c, tile_k(i), i < nt, slot);
+    issue_item<D, PT, (pos >= uint32_t(kChunk)), PAIR>(c, tile_k(i), i < nt, slot);
   };
   Slot<D> ring[NB];
-  // Start streaming before the Q set-up below.
+  // Start streaming before the Q digits are built.
   static_for<0, NB - 1>([&](auto uc) __attribute__((always_inline)) { issue(uc, 0u, ring[decltype(uc)::value]); });
 
-  // ---- Q digits (B operand of QK) and per-head score factors.
-  __syncthreads();  // q_s complete
-  i32x4 qd[NC][D / 64];
+  // ---- Q digits (B operand of QK) and per-head score factors.  A column's
+  // scale 2^kq comes from its head-row's whole Q row (with PAIR both tiles
+  // of a lane hold the same column).
+  i32x4 qd[NCQ][KS];
   float cql[HS];
   {
     int kq_lane = 0;
-#pragma unroll
-    for (int nc = 0; nc < NC; ++nc) {
-      const uint32_t col = 16u * nc + n;
-      const uint32_t dg = col / HS, h = col % HS;
-      const bool valid = col < 3u * HS && h < head_rows;
-      float qv[D / 4];
-      {
-        const float* src = q_s + (valid ? h : 0u) * D + g * (D / 4);
-#pragma unroll
-        for (int i = 0; i < D / 16; ++i) {
-          const float4 w = reinterpret_cast<const float4*>(src)[i];
-          qv[4 * i] = valid ? w.x : 0.f;
-          qv[4 * i + 1] = valid ? w.y : 0.f;
-          qv[4 * i + 2] = valid ? w.z : 0.f;
-          qv[4 * i + 3] = valid ? w.w : 0.f;
-        }
-      }
-      float amax = 0.f;
-#pragma unroll
-      for (int i = 0; i < D / 4; ++i) amax = fmaxf(amax, fabsf(qv[i]));
+    auto col_kq = [&](float amax) __attribute__((always_inline)) {
       amax = rows_max(amax);
       int kq = 0;
       if (amax > 0.f) {
         kq = 21 - __builtin_amdgcn_frexp_expf(amax);
         kq = kq < -100 ? -100 : (kq > 100 ? 100 : kq);
       }
+      return kq;
+    };
+    int kq_pair = 0;
+    if constexpr (PAIR) {
+      float amax = 0.f;
+#pragma unroll
+      for (int nc = 0; nc < NCQ; ++nc)
+#pragma unroll
+        for (int i = 0; i < 16 * KS; ++i) amax = fmaxf(amax, fabsf(qv[nc][i]));
+      kq_pair = col_kq(amax);
+    }
+#pragma unroll
+    for (int nc = 0; nc < NCQ; ++nc) {
+      const uint32_t col = PAIR ? n : 16u * nc + n;
+      const uint32_t dg = col / HS;
+      const bool valid = col < 3u * HS && col % HS < head_rows;
+      int kq = kq_pair;
+      if constexpr (!PAIR) {
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16 * KS; ++i) amax = fmaxf(amax, fabsf(qv[nc][i]));
+        kq = col_kq(amax);
+      }
       if (nc == 0) kq_lane = kq;
 #pragma unroll
-      for (int s = 0; s < D / 64; ++s) {
+      for (int s = 0; s < KS; ++s) {
         uint32_t w[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           uint32_t packed = 0;
 #pragma unroll
           for (int b = 0; b < 4; ++b) {
-            const int qi = int(__builtin_rintf(__builtin_amdgcn_ldexpf(qv[16 * s + 4 * j + b], kq)));
+            const int qi = int(__builtin_rintf(__builtin_amdgcn_ldexpf(qv[nc][16 * s + 4 * j + b], kq)));
             const int lo = int(int8_t(qi & 0xff));
             const int r1 = (qi - lo) >> 8;
             const int mid = int(int8_t(r1 & 0xff));
@@ -468,6 +508,7 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
   }
 
   uint8_t* const exch_w = wbase + n * L::kExchCol + 64u * g;              // C write base (MFMA view)
+  uint8_t* const exch_w2 = wbase + n * L::kExchCol + 8u * g;              // PAIR: summed C write base
   const uint8_t* const exch_r = wbase + 4u * lane;                        // lane-as-token read base
   uint8_t* const dig_w = wbase + L::kExch + lane;                         // digit write (lane-as-token)
   const uint8_t* const dig_r = wbase + L::kExch + n * L::kDigCol + 16u * g;  // B operand read
@@ -507,21 +548,38 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
     const bool real = i < nt;
     const bool full = real && t0 >= s0 && t0 + kTileTokens <= e_min;
     const bool tok_ok = full || (real && tok >= s0 && tok < e_max);
-    static_for<0, NC>([&](auto ncc) __attribute__((always_inline)) {
-      constexpr uint32_t nc = decltype(ncc)::value;
-      static_for<0, 4>([&](auto mbc) __attribute__((always_inline)) {
+    if constexpr (PAIR) {
+      // Rows 4g+e of M-block mb: e even = half 0, e odd = half 1 of tokens
+      // 8mb+2g (e < 2) and 8mb+2g+1; tile 0 gives the half-0 and tile 1 the
+      // half-1 dot products, summed exactly here.
+      static_for<0, 8>([&](auto mbc) __attribute__((always_inline)) {
         constexpr uint32_t mb = decltype(mbc)::value;
-        i32x4 cc = {0, 0, 0, 0};
-#pragma unroll
-        for (int s = 0; s < D / 64; ++s) {
-          const u32x4_t w = it.d[mb * (D / 64) + s];
-          const i32x4 av = {int(w[0]), int(w[1]), int(w[2]), int(w[3])};
-          cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, qd[nc][s], cc, 0, 0, 0);
-        }
-        const u32x4_t cw = {uint32_t(cc[0]), uint32_t(cc[1]), uint32_t(cc[2]), uint32_t(cc[3])};
-        *reinterpret_cast<u32x4_t*>(exch_w + (nc * 16 * L::kExchCol + 16 * mb)) = cw;
+        const u32x4_t w = it.d[mb];
+        const i32x4 av = {int(w[0]), int(w[1]), int(w[2]), int(w[3])};
+        const i32x4 zero = {0, 0, 0, 0};
+        const i32x4 c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, qd[0][0], zero, 0, 0, 0);
+        const i32x4 c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, qd[1][0], zero, 0, 0, 0);
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        const u32x2_t cw = {uint32_t(c0[0] + c1[1]), uint32_t(c0[2] + c1[3])};
+        *reinterpret_cast<u32x2_t*>(exch_w2 + 32 * mb) = cw;
       });
-    });
+    } else {
+      static_for<0, NC>([&](auto ncc) __attribute__((always_inline)) {
+        constexpr uint32_t nc = decltype(ncc)::value;
+        static_for<0, 4>([&](auto mbc) __attribute__((always_inline)) {
+          constexpr uint32_t mb = decltype(mbc)::value;
+          i32x4 cc = {0, 0, 0, 0};
+#pragma unroll
+          for (int s = 0; s < D / 64; ++s) {
+            const u32x4_t w = it.d[mb * (D / 64) + s];
+            const i32x4 av = {int(w[0]), int(w[1]), int(w[2]), int(w[3])};
+            cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, qd[nc][s], cc, 0, 0, 0);
+          }
+          const u32x4_t cw = {uint32_t(cc[0]), uint32_t(cc[1]), uint32_t(cc[2]), uint32_t(cc[3])};
+          *reinterpret_cast<u32x4_t*>(exch_w + (nc * 16 * L::kExchCol + 16 * mb)) = cw;
+        });
+      });
+    }
     int dv[HS][3];
     static_for<0, HS>([&](auto hc) __attribute__((always_inline)) {
       constexpr uint32_t h = decltype(hc)::value;
