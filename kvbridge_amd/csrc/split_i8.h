@@ -221,16 +221,57 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
   auto row_head = [&](uint32_t hh) __attribute__((always_inline)) {
     return size_t(hh / a.group) * a.q_heads + kv * a.group + hh % a.group;
   };
-  // Common case (<= 32 splits, one output per thread): the thread's
-  // numerators and its wave's (m_j, l_j) are requested together, so the
-  // whole merge costs one memory round trip.
-  const bool one_pass = a.splits <= kCh && outs <= 64u * NW;
-  float pre[kCh];
-  if (one_pass && tid < outs) {
-    const float* base = scratch + row_head(tid / D) * a.splits * W + 2 + tid % D;
+  // Common case (<= 32 splits, one output per thread, one head-row per
+  // wave): straight-line code that requests every operand at once -- the
+  // wave's (m_j, l_j) and the thread's 32 numerators, split indices clamped
+  // instead of branched on -- so the merge costs one memory round trip.
+  if (a.splits <= kCh && outs <= 64u * NW && head_rows <= uint32_t(NW)) {
+    const uint32_t jmax = a.splits - 1u;
+    const bool fw = wave < head_rows;
+    const float* fb = scratch + row_head(fw ? wave : 0u) * a.splits * W;
+    const uint32_t jl = lane < a.splits ? lane : jmax;
+    const float mj = ld_agent(fb + size_t(jl) * W);
+    const float lj = ld_agent(fb + size_t(jl) * W + 1);
+    const bool ot = tid < outs;
+    const uint32_t o = ot ? tid : 0u;
+    const float* nb = scratch + row_head(o / D) * a.splits * W + 2 + o % D;
+    float pre[kCh];
 #pragma unroll
-    for (uint32_t j = 0; j < kCh; ++j) pre[j] = j < a.splits ? ld_agent(base + size_t(j) * W) : 0.f;
+    for (uint32_t j = 0; j < kCh; ++j) pre[j] = ld_agent(nb + size_t(j < jmax ? j : jmax) * W);
+    if (fw) {
+      const bool in = lane < a.splits;
+      const float mx = wave_max(in ? mj : neg_inf());
+      const float f = in && lj > 0.f ? exp_e(mj - mx) : 0.f;
+      const float lsum = wave_sum(f * lj);
+      if (lane < kCh) f_s[wave * kCh + lane] = f;
+      if (lane == 0) {
+        ml_s[2 * wave] = mx;
+        ml_s[2 * wave + 1] = lsum;
+      }
+    }
+    __syncthreads();
+    if (ot) {
+      const uint32_t hh = o / D, d = o % D;
+      const float* fh = f_s + hh * kCh;
+      float nacc = 0.f;
+#pragma unroll
+      for (uint32_t j = 0; j < kCh; ++j) nacc = fmaf(fh[j], j <= jmax ? pre[j] : 0.f, nacc);
+      const size_t rh = row_head(hh);
+      const float lsum = ml_s[2 * hh + 1];
+      if (d == 0) {
+        a.m[rh] = ml_s[2 * hh];
+        a.l[rh] = lsum;
+      }
+      a.n[rh * D + d] = nacc;
+      if (a.out_type != 0) {
+        const float ov = lsum > 0.f ? nacc / lsum : 0.f;
+        if (a.out_type == 1) static_cast<float*>(a.out)[rh * D + d] = ov;
+        else static_cast<_Float16*>(a.out)[rh * D + d] = (_Float16)ov;
+      }
+    }
+    return;
   }
+  // General case: passes of 32 splits; the running numerator goes through n.
   for (uint32_t j0 = 0; j0 < a.splits; j0 += kCh) {
     const uint32_t cnt = a.splits - j0 < kCh ? a.splits - j0 : kCh;
     for (uint32_t hh = wave; hh < head_rows; hh += NW) {
@@ -260,17 +301,15 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
       const float* fh = f_s + hh * kCh;
       const size_t rh = row_head(hh);
       float nacc = 0.f;
-      if (one_pass) {
-#pragma unroll
-        for (uint32_t j = 0; j < kCh; ++j) nacc = fmaf(fh[j], pre[j], nacc);
-      } else {
+      {
         const float* base = scratch + rh * a.splits * W + 2 + d;
+        const uint32_t jm = j0 + cnt - 1u;
         float nv[kCh];
 #pragma unroll
-        for (uint32_t j = 0; j < kCh; ++j) nv[j] = j < cnt ? ld_agent(base + size_t(j0 + j) * W) : 0.f;
+        for (uint32_t j = 0; j < kCh; ++j) nv[j] = ld_agent(base + size_t(j0 + j < jm ? j0 + j : jm) * W);
         if (j0 != 0) nacc = a.n[rh * D + d];
 #pragma unroll
-        for (uint32_t j = 0; j < kCh; ++j) nacc = fmaf(fh[j], nv[j], nacc);
+        for (uint32_t j = 0; j < kCh; ++j) nacc = fmaf(fh[j], j < cnt ? nv[j] : 0.f, nacc);
       }
       if (j0 + kCh < a.splits) {
         a.n[rh * D + d] = nacc;  // running numerator, re-read by this thread next pass
