@@ -36,4 +36,56 @@ void decode_attention(const Shape&, const DeviceInput&, unsigned split_tokens,
                       float* scratch, float* m, float* l, float* n, void* out,
                       OutputType out_type, hipStream_t stream);
 
+// ---- batched ragged decode: many independent sequences over one paged pool.
+// Sequence b has `rows` query rows (q_heads heads each, sharing its KV) that
+// attend to its own tokens [0, T_b): T_b = seq_starts[b+1] - seq_starts[b],
+// its key positions are k_positions[seq_starts[b] ..], and its logical page
+// p is physical page page_table[page_offsets[b] + p] of the shared pool.
+// Each sequence runs max(1, ceil(T_b / split_tokens)) splits; the partial
+// stride per sequence is batch_split_count (the split count of max_tokens),
+// and splits past a sequence's own count hold empty partials.  The device
+// metadata is read by the kernels (the call is graph-capturable with
+// changing lengths); indices are clamped to total_tokens / table_entries and
+// T_b to max_tokens, so a malformed batch cannot read out of bounds.
+struct BatchShape {
+  unsigned batch, rows, q_heads, kv_heads, dim, page_tokens, pages;
+  unsigned max_tokens;     // bound on every T_b: sizes the grid and the scratch
+  unsigned total_tokens;   // k_positions entries
+  unsigned table_entries;  // page_table entries
+  unsigned split_tokens;   // tokens per split
+  float scale;
+  bool int8;
+};
+
+struct BatchInput {
+  const float* q;               // [batch][rows][q_heads][dim]
+  const int64_t* q_positions;   // [batch][rows]
+  const uint32_t* seq_starts;   // [batch + 1], nondecreasing
+  const uint32_t* page_offsets; // [batch]
+  const int64_t* k_positions;   // [total_tokens], nondecreasing within a sequence
+  const uint32_t* page_table;   // [table_entries]
+  const void* k;                // shared pool, layouts as DeviceInput
+  const void* v;
+  const float* k_scales;
+  const float* v_scales;
+};
+
+// nullptr when valid, else the first failed rule (never throws).
+const char* batch_shape_error(const BatchShape&) noexcept;
+// Partial stride per sequence (split count of max_tokens); validates.
+unsigned batch_split_count(const BatchShape&);
+// batch * rows * q_heads * batch_split_count * (dim + 2) floats; validates.
+size_t batch_scratch_elements(const BatchShape&);
+// batch * rows * q_heads (m, l); times dim for n and out; validates.
+size_t batch_output_scalar_elements(const BatchShape&);
+
+// Split partials + LSE merge (+ normalized output) of every sequence.  With
+// counters (batch * kv_heads uint32, zero before the first call and left
+// zero) the int8-MFMA kernel serves the whole call in one launch where it
+// supports the shape; with counters == nullptr, or otherwise, split and merge
+// run as two launches.
+void decode_attention_batched(const BatchShape&, const BatchInput&, float* scratch,
+                              uint32_t* counters, float* m, float* l, float* n, void* out,
+                              OutputType out_type, hipStream_t stream);
+
 }  // namespace kvbridge

@@ -115,6 +115,58 @@ int kvb_decode_attention(const kvb_shape* s, const kvb_device_input* in, uint32_
 int kvb_decode_attention_fused(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens,
                                float* scratch, uint32_t* counters, float* m, float* l, float* n, void* out,
                                int out_type, void* stream);
+/* Extension (no counterpart in the reference library, which serves one
+ * sequence per call; for batched serving loops and the ragged-batch
+ * workloads): a batch of independent decode sequences over one shared paged
+ * KV pool, in one call.  Mirrors kvbridge::BatchShape / BatchInput
+ * (include/kvbridge/attention_ext.h, which documents the layout): sequence b
+ * attends to its tokens [0, T_b), T_b = seq_starts[b+1] - seq_starts[b], its
+ * logical page p is physical page page_table[page_offsets[b] + p], and it runs
+ * max(1, ceil(T_b / split_tokens)) splits.  seq_starts and page_offsets are
+ * device arrays read by the kernels (graph-capturable with changing
+ * lengths); every index is clamped to total_tokens / table_entries and T_b
+ * to max_tokens. */
+typedef struct kvb_batch_shape {
+  uint32_t batch, rows, q_heads, kv_heads, dim, page_tokens, pages;
+  uint32_t max_tokens, total_tokens, table_entries, split_tokens;
+  float scale;
+  uint32_t int8;
+} kvb_batch_shape;
+
+typedef struct kvb_batch_input {
+  const float* q;
+  const int64_t* q_positions;
+  const uint32_t* seq_starts;
+  const uint32_t* page_offsets;
+  const int64_t* k_positions;
+  const uint32_t* page_table;
+  const void* k;
+  const void* v;
+  const float* k_scales;
+  const float* v_scales;
+} kvb_batch_input;
+
+/* NULL when valid, else the first failed rule's message. */
+const char* kvb_batch_shape_error(const kvb_batch_shape* s);
+/* Partial stride per sequence (split count of max_tokens). */
+int kvb_batch_split_count(const kvb_batch_shape* s, uint32_t* splits);
+/* batch * rows * q_heads * kvb_batch_split_count * (dim + 2) floats. */
+int kvb_batch_scratch_elements(const kvb_batch_shape* s, size_t* elements);
+/* batch * rows * q_heads: elements of m and l (times dim: n and out). */
+int kvb_batch_output_scalar_elements(const kvb_batch_shape* s, size_t* elements);
+/* Split partials + log-sum-exp merge of every sequence into m, l, n and
+ * out (KVB_OUT_*), in the batch's row-head order.  counters == NULL: two
+ * launches (split, merge).  counters != NULL (batch * kv_heads uint32, zero
+ * before the first call and left zero by every call): one launch where the
+ * int8-MFMA kernel serves the shape, the last work-group of each
+ * (sequence, kv head) merging its splits; otherwise two launches. */
+int kvb_decode_attention_batched(const kvb_batch_shape* s, const kvb_batch_input* in, float* scratch,
+                                 uint32_t* counters, float* m, float* l, float* n, void* out, int out_type,
+                                 void* stream);
+/* Extension (diagnostic): name of the split kernel instance the batched call
+ * would launch ("" if the arguments are invalid). */
+const char* kvb_batch_kernel_name(const kvb_batch_shape* s, const kvb_batch_input* in, int fused);
+
 /* Extension (diagnostic): which split kernel kvb_split_attention would run for
  * these arguments: KVB_KERNEL_TILED_MFMA or KVB_KERNEL_GENERIC; 0 if invalid. */
 int kvb_selected_kernel(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens);

@@ -13,6 +13,8 @@ from __future__ import annotations
 import ctypes
 
 from ._capi import (  # noqa: F401
+    BatchInput,
+    BatchShape,
     KVB_KERNEL_GENERIC,
     KVB_KERNEL_TILED_MFMA,
     KVB_OUT_F16,
@@ -168,3 +170,54 @@ def selected_kernel_name(s: Shape, inp: DeviceInput, split_tokens: int, fused: b
 def hbm_read_probe(src, nbytes: int, sink, blocks: int, stream=None) -> None:
     """Diagnostic streaming read of nbytes of device memory (see kvb_hbm_read_probe)."""
     check(load().kvb_hbm_read_probe(_ptr(src), nbytes, _ptr(sink), blocks, _stream(stream)))
+
+
+# ---- batched ragged decode (kvb_decode_attention_batched) ---------------------
+
+def make_batch_shape(batch, rows, q_heads, kv_heads, dim, page_tokens, pages, max_tokens, total_tokens,
+                     table_entries, split_tokens, scale, int8=True) -> BatchShape:
+    return BatchShape(batch, rows, q_heads, kv_heads, dim, page_tokens, pages, max_tokens, total_tokens,
+                      table_entries, split_tokens, float(scale), 1 if int8 else 0)
+
+
+def batch_shape_error(s: BatchShape):
+    r = load().kvb_batch_shape_error(ctypes.byref(s))
+    return None if r is None else r.decode()
+
+
+def batch_split_count(s: BatchShape) -> int:
+    out = ctypes.c_uint32()
+    check(load().kvb_batch_split_count(ctypes.byref(s), ctypes.byref(out)))
+    return out.value
+
+
+def batch_scratch_elements(s: BatchShape) -> int:
+    out = ctypes.c_size_t()
+    check(load().kvb_batch_scratch_elements(ctypes.byref(s), ctypes.byref(out)))
+    return out.value
+
+
+def batch_output_scalar_elements(s: BatchShape) -> int:
+    out = ctypes.c_size_t()
+    check(load().kvb_batch_output_scalar_elements(ctypes.byref(s), ctypes.byref(out)))
+    return out.value
+
+
+def batch_input(q, q_positions, seq_starts, page_offsets, k_positions, page_table, k, v, k_scales=None,
+                v_scales=None) -> BatchInput:
+    """Build a kvb_batch_input from device tensors (or raw integer pointers)."""
+    return BatchInput(*(_ptr(x) for x in (q, q_positions, seq_starts, page_offsets, k_positions, page_table,
+                                          k, v, k_scales, v_scales)))
+
+
+def decode_attention_batched(s: BatchShape, inp: BatchInput, scratch, m, l, n, out=None,
+                             out_type: int = KVB_OUT_NONE, counters=None, stream=None) -> None:
+    """Batched decode (kvb_decode_attention_batched): one launch when `counters`
+    (batch * kv_heads uint32 zeros, left zero) is given and the int8 kernel
+    serves the shape, else split + merge launches."""
+    check(load().kvb_decode_attention_batched(ctypes.byref(s), ctypes.byref(inp), _ptr(scratch), _ptr(counters),
+                                              _ptr(m), _ptr(l), _ptr(n), _ptr(out), out_type, _stream(stream)))
+
+
+def batch_kernel_name(s: BatchShape, inp: BatchInput, fused: bool = False) -> str:
+    return load().kvb_batch_kernel_name(ctypes.byref(s), ctypes.byref(inp), int(fused)).decode()

@@ -58,6 +58,31 @@ class DeviceInput(ctypes.Structure):
     ]
 
 
+class BatchShape(ctypes.Structure):
+    """kvb_batch_shape: mirrors kvbridge::BatchShape (include/kvbridge/attention_ext.h)."""
+
+    _fields_ = [(n, ctypes.c_uint32) for n in
+                ("batch", "rows", "q_heads", "kv_heads", "dim", "page_tokens", "pages",
+                 "max_tokens", "total_tokens", "table_entries", "split_tokens")] + \
+               [("scale", ctypes.c_float), ("int8", ctypes.c_uint32)]
+
+    def as_tuple(self):
+        return tuple(getattr(self, f) for f, _ in self._fields_)
+
+    def copy(self, **changes) -> "BatchShape":
+        vals = {f: getattr(self, f) for f, _ in self._fields_}
+        vals.update(changes)
+        return BatchShape(**vals)
+
+
+class BatchInput(ctypes.Structure):
+    """kvb_batch_input: mirrors kvbridge::BatchInput (include/kvbridge/attention_ext.h)."""
+
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("q", "q_positions", "seq_starts", "page_offsets", "k_positions", "page_table",
+                 "k", "v", "k_scales", "v_scales")]
+
+
 class KvbError(Exception):
     """Base class; the subclasses mirror std::invalid_argument / std::runtime_error."""
 
@@ -73,6 +98,8 @@ class KvbRuntimeError(KvbError, RuntimeError):
 # (name, restype, argtypes) for every function declared in include/kvbridge_c.h.
 _SP = ctypes.POINTER(Shape)
 _IP = ctypes.POINTER(DeviceInput)
+_BSP = ctypes.POINTER(BatchShape)
+_BIP = ctypes.POINTER(BatchInput)
 _VP = ctypes.c_void_p
 _U32 = ctypes.c_uint32
 _INT = ctypes.c_int
@@ -101,6 +128,12 @@ SIGNATURES = [
     ("kvb_selected_kernel", _INT, [_SP, _IP, _U32]),
     ("kvb_selected_kernel_name", ctypes.c_char_p, [_SP, _IP, _U32, _INT]),
     ("kvb_hbm_read_probe", _INT, [_VP, ctypes.c_size_t, _VP, _U32, _VP]),
+    ("kvb_batch_shape_error", ctypes.c_char_p, [_BSP]),
+    ("kvb_batch_split_count", _INT, [_BSP, ctypes.POINTER(_U32)]),
+    ("kvb_batch_scratch_elements", _INT, [_BSP, ctypes.POINTER(ctypes.c_size_t)]),
+    ("kvb_batch_output_scalar_elements", _INT, [_BSP, ctypes.POINTER(ctypes.c_size_t)]),
+    ("kvb_decode_attention_batched", _INT, [_BSP, _BIP, _VP, _VP, _VP, _VP, _VP, _VP, _INT, _VP]),
+    ("kvb_batch_kernel_name", ctypes.c_char_p, [_BSP, _BIP, _INT]),
 ]
 
 _lib = None

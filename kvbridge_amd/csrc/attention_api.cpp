@@ -76,4 +76,14 @@ void decode_attention(const Shape& s, const DeviceInput& in, unsigned split_toke
   check(kvb_decode_attention(&cs, &ci, split_tokens, scratch, m, l, n, out, int(out_type), stream));
 }
 
+void decode_attention_batched(const BatchShape& b, const BatchInput& in, float* scratch, uint32_t* counters,
+                              float* m, float* l, float* n, void* out, OutputType out_type, hipStream_t stream) {
+  const kvb_batch_shape cs{b.batch,      b.rows,         b.q_heads,      b.kv_heads,     b.dim,
+                           b.page_tokens, b.pages,        b.max_tokens,   b.total_tokens, b.table_entries,
+                           b.split_tokens, b.scale,       b.int8 ? 1u : 0u};
+  const kvb_batch_input ci{in.q,          in.q_positions, in.seq_starts, in.page_offsets, in.k_positions,
+                           in.page_table, in.k,           in.v,          in.k_scales,     in.v_scales};
+  check(kvb_decode_attention_batched(&cs, &ci, scratch, counters, m, l, n, out, int(out_type), stream));
+}
+
 }  // namespace kvbridge

@@ -93,6 +93,54 @@ int guarded(F&& f) {
   }
 }
 
+kvbridge::BatchShape to_batch_shape(const kvb_batch_shape& b) {
+  return kvbridge::BatchShape{b.batch,      b.rows,         b.q_heads,       b.kv_heads,     b.dim,
+                              b.page_tokens, b.pages,        b.max_tokens,    b.total_tokens, b.table_entries,
+                              b.split_tokens, b.scale,       b.int8 != 0};
+}
+
+// One sequence of max_tokens tokens: the shape the per-sequence kernels see.
+kvbridge::Shape batch_sequence_shape(const kvbridge::BatchShape& b) {
+  return kvbridge::Shape{b.rows, b.q_heads, b.kv_heads, b.dim, b.page_tokens, b.pages,
+                         b.max_tokens, 0, b.max_tokens, b.scale, b.int8};
+}
+
+kvbridge::DeviceInput batch_device_input(const kvb_batch_input& in) {
+  return kvbridge::DeviceInput{in.q, in.q_positions, in.k_positions, in.page_table,
+                               in.k, in.v, in.k_scales, in.v_scales};
+}
+
+const char* batch_launch_error(const kvbridge::BatchShape& b, const kvb_batch_input& in, const void* scratch,
+                               const void* m, const void* l, const void* n) {
+  if (const char* e = kvbridge::batch_shape_error(b)) return e;
+  if (!scratch || !m || !l || !n) return "scratch, m, l and n must be non-null device buffers";
+  if (!in.q || !in.q_positions || !in.seq_starts || !in.page_offsets || !in.k_positions || !in.page_table ||
+      !in.k || !in.v || (b.int8 && (!in.k_scales || !in.v_scales)))
+    return "attention input device buffers must be non-null";
+  if (b.int8 && b.dim % 4 == 0 && b.page_tokens % 4 == 0 &&
+      ((reinterpret_cast<uintptr_t>(in.k) % 4) || (reinterpret_cast<uintptr_t>(in.v) % 4)))
+    return "vectorized INT8 K/V buffers must be 4-byte aligned";
+  return nullptr;
+}
+
+kvb::SplitArgs batch_split_args(const kvbridge::BatchShape& b, const kvb_batch_input& in, float* scratch) {
+  const kvbridge::Shape s = batch_sequence_shape(b);
+  kvb::SplitArgs a = kvb::make_split_args(s, batch_device_input(in), b.split_tokens,
+                                          kvbridge::batch_split_count(b), scratch);
+  a.seq_starts = in.seq_starts;
+  a.page_offsets = in.page_offsets;
+  a.batch = b.batch;
+  a.total_tokens = b.total_tokens;
+  a.table_entries = b.table_entries;
+  a.max_tokens = b.max_tokens;
+  return a;
+}
+
+// The batched split kernel: int8 MFMA where it applies, else the generic one.
+bool batch_uses_i8(const kvbridge::BatchShape& b, const kvb_batch_input& in, const kvb::SplitArgs& a) {
+  return kvb::tiled_supported(batch_sequence_shape(b), batch_device_input(in)) && kvb::i8_supported(a);
+}
+
 }  // namespace
 
 namespace kvb {
@@ -138,7 +186,10 @@ hipError_t launch_split_fast(const SplitArgs& a, hipStream_t stream) {
 }
 
 const char* split_kernel_name(const SplitArgs& a, bool tiled, bool int8) {
-  if (!tiled) return int8 ? "split_generic_kernel<true>" : "split_generic_kernel<false>";
+  if (!tiled) {
+    if (a.seq_starts) return int8 ? "split_generic_kernel<true, true>" : "split_generic_kernel<false, true>";
+    return int8 ? "split_generic_kernel<true, false>" : "split_generic_kernel<false, false>";
+  }
   if (!force_f16() && i8_supported(a)) return i8_kernel_name(a);
   return lds_kernel_name(a);
 }
@@ -406,6 +457,76 @@ const char* kvb_selected_kernel_name(const kvb_shape* sp, const kvb_device_input
   static uint32_t dummy_counter;  // only its non-nullness is read
   if (fused && kvb::tiled_supported(s, in) && kvb::i8_fusable(a)) a.counters = &dummy_counter;
   return kvb::split_kernel_name(a, kvb::tiled_supported(s, in), s.int8);
+}
+
+const char* kvb_batch_shape_error(const kvb_batch_shape* s) {
+  if (!s) return "shape pointer must be non-null";
+  return kvbridge::batch_shape_error(to_batch_shape(*s));
+}
+
+int kvb_batch_split_count(const kvb_batch_shape* s, uint32_t* splits) {
+  return guarded([&]() -> int {
+    if (!s || !splits) return fail(KVB_EINVAL, "shape and output pointers must be non-null");
+    *splits = kvbridge::batch_split_count(to_batch_shape(*s));
+    return KVB_OK;
+  });
+}
+
+int kvb_batch_scratch_elements(const kvb_batch_shape* s, size_t* elements) {
+  return guarded([&]() -> int {
+    if (!s || !elements) return fail(KVB_EINVAL, "shape and output pointers must be non-null");
+    *elements = kvbridge::batch_scratch_elements(to_batch_shape(*s));
+    return KVB_OK;
+  });
+}
+
+int kvb_batch_output_scalar_elements(const kvb_batch_shape* s, size_t* elements) {
+  return guarded([&]() -> int {
+    if (!s || !elements) return fail(KVB_EINVAL, "shape and output pointers must be non-null");
+    *elements = kvbridge::batch_output_scalar_elements(to_batch_shape(*s));
+    return KVB_OK;
+  });
+}
+
+int kvb_decode_attention_batched(const kvb_batch_shape* sp, const kvb_batch_input* ip, float* scratch,
+                                 uint32_t* counters, float* m, float* l, float* n, void* out, int out_type,
+                                 void* stream) {
+  return guarded([&]() -> int {
+    if (!sp || !ip) return fail(KVB_EINVAL, "shape and input descriptors must be non-null");
+    const kvbridge::BatchShape b = to_batch_shape(*sp);
+    if (const char* e = batch_launch_error(b, *ip, scratch, m, l, n)) return fail(KVB_EINVAL, e);
+    if (out_type != KVB_OUT_NONE && out_type != KVB_OUT_F32 && out_type != KVB_OUT_F16)
+      return fail(KVB_EINVAL, "unknown output type");
+    if (out_type != KVB_OUT_NONE && !out) return fail(KVB_EINVAL, "output buffer must be non-null");
+    const auto st = static_cast<hipStream_t>(stream);
+    kvb::SplitArgs a = batch_split_args(b, *ip, scratch);
+    const bool i8 = batch_uses_i8(b, *ip, a);
+    if (i8 && counters) {
+      a.counters = counters;
+      a.m = m;
+      a.l = l;
+      a.n = n;
+      a.out = out;
+      a.out_type = out_type;
+      return hip_status(kvb::launch_split_i8(a, st), "fused batched decode launch");
+    }
+    const hipError_t e = i8 ? kvb::launch_split_i8(a, st) : kvb::launch_split_generic(a, b.int8, st);
+    if (const int rc = hip_status(e, "batched split launch"); rc != KVB_OK) return rc;
+    const uint32_t row_heads = b.batch * b.rows * b.q_heads;
+    return hip_status(kvb::launch_merge(row_heads, b.dim, a.splits, scratch, m, l, n, out, out_type, st),
+                      "batched merge launch");
+  });
+}
+
+const char* kvb_batch_kernel_name(const kvb_batch_shape* sp, const kvb_batch_input* ip, int fused) {
+  if (!sp || !ip) return "";
+  const kvbridge::BatchShape b = to_batch_shape(*sp);
+  if (kvbridge::batch_shape_error(b)) return "";
+  kvb::SplitArgs a = batch_split_args(b, *ip, nullptr);
+  const bool i8 = batch_uses_i8(b, *ip, a);
+  static uint32_t dummy_counter;  // only its non-nullness is read
+  if (fused && i8) a.counters = &dummy_counter;
+  return kvb::split_kernel_name(a, i8, b.int8);
 }
 
 }  // extern "C"

@@ -32,6 +32,19 @@ struct SplitArgs {
   float* n;
   void* out;
   int out_type;
+  // Batched call (kvb_decode_attention_batched): non-null seq_starts makes
+  // grid.z the sequence index b, and every work-group first rebases these
+  // arguments on sequence b (rebase_sequence, batch.h).  q, q_positions and
+  // the outputs then hold `batch` consecutive blocks of rows * q_heads
+  // row-heads, k_positions and page_table are concatenations indexed through
+  // seq_starts / page_offsets, and `splits` is the partial stride of every
+  // sequence (the split count of max_tokens).
+  const uint32_t* seq_starts;    // [batch + 1] token offsets into k_positions
+  const uint32_t* page_offsets;  // [batch] first page-table entry of each sequence
+  uint32_t batch;
+  uint32_t total_tokens;         // k_positions entries (device indices are clamped to it)
+  uint32_t table_entries;        // page_table entries (likewise)
+  uint32_t max_tokens;           // bound on every sequence's token count
 };
 
 SplitArgs make_split_args(const kvbridge::Shape& s, const kvbridge::DeviceInput& in,

@@ -7,8 +7,10 @@
 // weighted by v_scale), evaluated as an online softmax over 256-token chunks
 // so that one work-group can cover a split of any length.
 //
-// Grid: x = row * q_heads + head, y = split.  Block: 256 threads (4 waves).
+// Grid: x = row * q_heads + head, y = split, z = sequence of a batched call.
+// Block: 256 threads (4 waves).
 #include "kernels.h"
+#include "batch.h"
 #include "device_common.h"
 
 namespace kvb {
@@ -46,8 +48,9 @@ __device__ __forceinline__ float kv_value(const void* base, uint32_t i) {
   else return static_cast<const float*>(base)[i];
 }
 
-template <bool kInt8>
+template <bool kInt8, bool VARLEN>
 __global__ __launch_bounds__(kThreads) void split_generic_kernel(SplitArgs a) {
+  if constexpr (VARLEN) rebase_sequence(a, blockIdx.z);
   __shared__ float q_s[256];
   __shared__ float pw_s[kThreads];
   __shared__ uint32_t vbase_s[kThreads];
@@ -117,19 +120,30 @@ __global__ __launch_bounds__(kThreads) void split_generic_kernel(SplitArgs a) {
 }  // namespace
 
 hipError_t launch_split_generic(const SplitArgs& a, bool int8, hipStream_t stream) {
-  const dim3 grid(a.rows * a.q_heads, a.splits);
-  if (int8)
-    hipLaunchKernelGGL(split_generic_kernel<true>, grid, dim3(kThreads), 0, stream, a);
+  const bool varlen = a.seq_starts != nullptr;
+  const dim3 grid(a.rows * a.q_heads, a.splits, varlen ? a.batch : 1u);
+  if (int8 && varlen)
+    hipLaunchKernelGGL((split_generic_kernel<true, true>), grid, dim3(kThreads), 0, stream, a);
+  else if (int8)
+    hipLaunchKernelGGL((split_generic_kernel<true, false>), grid, dim3(kThreads), 0, stream, a);
+  else if (varlen)
+    hipLaunchKernelGGL((split_generic_kernel<false, true>), grid, dim3(kThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL(split_generic_kernel<false>, grid, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((split_generic_kernel<false, false>), grid, dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 
 hipError_t preload_generic() {
+  const void* fns[] = {reinterpret_cast<const void*>(&split_generic_kernel<true, false>),
+                       reinterpret_cast<const void*>(&split_generic_kernel<false, false>),
+                       reinterpret_cast<const void*>(&split_generic_kernel<true, true>),
+                       reinterpret_cast<const void*>(&split_generic_kernel<false, true>)};
   hipFuncAttributes attr{};
-  hipError_t e = hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_generic_kernel<true>));
-  if (e != hipSuccess) return e;
-  return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_generic_kernel<false>));
+  for (const void* f : fns) {
+    const hipError_t e = hipFuncGetAttributes(&attr, f);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace kvb

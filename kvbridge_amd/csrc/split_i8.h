@@ -41,6 +41,7 @@
 #include <cstdint>
 
 #include "kernels.h"
+#include "batch.h"
 #include "device_common.h"
 #include "lds_stream.h"
 
@@ -331,12 +332,20 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
   }
 }
 
-template <int D, int NW, int NB, bool PT, int HS, bool FUSED>
+// VARLEN: batched call, grid.z = sequence (arguments rebased per work-group).
+template <int D, int NW, int NB, bool PT, int HS, bool FUSED, bool VARLEN>
 __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
-    SplitArgs a, const float* __restrict__ q, const int64_t* __restrict__ qpos,
-    const int64_t* __restrict__ kpos, const uint32_t* __restrict__ table,
+    SplitArgs a_in, const float* __restrict__ q_in, const int64_t* __restrict__ qpos_in,
+    const int64_t* __restrict__ kpos_in, const uint32_t* __restrict__ table_in,
     const int8_t* __restrict__ kdata, const int8_t* __restrict__ vdata,
-    const float* __restrict__ kscale, const float* __restrict__ vscale, float* __restrict__ scratch) {
+    const float* __restrict__ kscale, const float* __restrict__ vscale, float* __restrict__ scratch_in) {
+  SplitArgs a = a_in;
+  if constexpr (VARLEN) rebase_sequence(a, blockIdx.z);
+  const float* __restrict__ q = VARLEN ? a.q : q_in;
+  const int64_t* __restrict__ qpos = VARLEN ? a.q_positions : qpos_in;
+  const int64_t* __restrict__ kpos = VARLEN ? a.k_positions : kpos_in;
+  const uint32_t* __restrict__ table = VARLEN ? a.page_table : table_in;
+  float* __restrict__ scratch = VARLEN ? a.scratch : scratch_in;
   using L = I8Layout<D, NW, HS>;
   constexpr int NC = L::NC;  // MFMA column tiles of the digit columns (PV; QK unless PAIR)
   // Paired-row QK (dim 128, <= 4 head-rows): MFMA row m of M-block mb is
@@ -376,8 +385,10 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
   c.lane = lane;
   c.lg_p = 31u - __builtin_clz(a.page_tokens);  // page_tokens is a power of two
   {
+    // Page-table window of the split (no load for an empty split, whose
+    // lp_lo may be one past the last page).
     const uint32_t lp = c.lp_lo + lane;
-    c.ptab = lp <= c.lp_hi ? table[lp] : 0u;
+    c.ptab = s1 > s0 && lp <= c.lp_hi ? table[lp] : 0u;
   }
   if constexpr (PT) {
     c.voff_k = PAIR ? 128u * (n >> 1) + 64u * (n & 1u) + 16u * g
@@ -833,25 +844,33 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
 
 template <int D, int NW, int NB, int HS>
 hipError_t launch_cfg(const SplitArgs& a, hipStream_t stream) {
-  const dim3 grid(a.splits, a.kv_heads);
-  const bool pt = a.page_tokens >= kTileTokens, fused = a.counters != nullptr;
-  if (pt && fused)
-    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, true, HS, true>), grid, dim3(64 * NW), 0, stream, KVB_I8_ARGS);
+  const bool pt = a.page_tokens >= kTileTokens, fused = a.counters != nullptr, varlen = a.seq_starts != nullptr;
+  const dim3 grid(a.splits, a.kv_heads, varlen ? a.batch : 1u);
+  const dim3 block(64 * NW);
+  if (varlen && !pt) return hipErrorInvalidValue;  // batched calls need whole-tile pages (i8_supported)
+  if (varlen && fused)
+    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, true, HS, true, true>), grid, block, 0, stream, KVB_I8_ARGS);
+  else if (varlen)
+    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, true, HS, false, true>), grid, block, 0, stream, KVB_I8_ARGS);
+  else if (pt && fused)
+    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, true, HS, true, false>), grid, block, 0, stream, KVB_I8_ARGS);
   else if (pt)
-    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, true, HS, false>), grid, dim3(64 * NW), 0, stream, KVB_I8_ARGS);
+    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, true, HS, false, false>), grid, block, 0, stream, KVB_I8_ARGS);
   else if (fused)
-    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, false, HS, true>), grid, dim3(64 * NW), 0, stream, KVB_I8_ARGS);
+    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, false, HS, true, false>), grid, block, 0, stream, KVB_I8_ARGS);
   else
-    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, false, HS, false>), grid, dim3(64 * NW), 0, stream, KVB_I8_ARGS);
+    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, false, HS, false, false>), grid, block, 0, stream, KVB_I8_ARGS);
   return hipGetLastError();
 }
 
 template <int D, int NW, int NB, int HS>
 hipError_t preload_cfg() {
-  const void* fns[] = {reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS, false>),
-                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, false, HS, false>),
-                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS, true>),
-                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, false, HS, true>)};
+  const void* fns[] = {reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS, false, false>),
+                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, false, HS, false, false>),
+                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS, true, false>),
+                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, false, HS, true, false>),
+                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS, false, true>),
+                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS, true, true>)};
   hipFuncAttributes attr{};
   for (const void* f : fns) {
     const hipError_t e = hipFuncGetAttributes(&attr, f);

@@ -38,13 +38,14 @@ int i8_config(const SplitArgs& a) {
 
 }  // namespace
 
-// head_rows <= 8 (<= 4 at dim 256); page_tokens a power of two >= 16; the
-// small-page path addresses K/V with 32-bit offsets.
+// head_rows <= 8 (<= 4 at dim 256); page_tokens a power of two >= 16 (>= 64
+// for batched calls); the small-page path addresses K/V with 32-bit offsets.
 bool i8_supported(const SplitArgs& a) {
   const uint32_t hr = a.rows * a.group, P = a.page_tokens;
   if (hr > 8 || (a.dim == 256 && hr > 4)) return false;
   if (a.dim != 64 && a.dim != 128 && a.dim != 256) return false;
   if (P < 16 || (P & (P - 1u)) != 0) return false;
+  if (a.seq_starts && P < kTiles) return false;  // batched calls: whole-tile pages only
   if (P < kTiles && uint64_t(a.pages) * a.kv_heads * P * a.dim >= (uint64_t(1) << 32)) return false;
   return true;
 }
@@ -64,9 +65,9 @@ hipError_t launch_split_i8(const SplitArgs& a, hipStream_t stream) {
 const char* i8_kernel_name(const SplitArgs& a) {
   static thread_local char buf[112];
   const int cfg = i8_config(a);
-  std::snprintf(buf, sizeof(buf), "split_i8_kernel<%u,%d,%d,%s,%d,%s>", a.dim, cfg / 10, cfg % 10,
+  std::snprintf(buf, sizeof(buf), "split_i8_kernel<%u,%d,%d,%s,%d,%s,%s>", a.dim, cfg / 10, cfg % 10,
                 a.page_tokens >= kTiles ? "true" : "false", a.rows * a.group <= 4 ? 4 : 8,
-                a.counters != nullptr ? "true" : "false");
+                a.counters != nullptr ? "true" : "false", a.seq_starts != nullptr ? "true" : "false");
   return buf;
 }
 

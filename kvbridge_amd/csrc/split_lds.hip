@@ -227,8 +227,9 @@ __global__ __launch_bounds__(64 * NW) void split_lds_kernel(
 
   // ---- page-table window, then start streaming before anything else.
   {
+    // No table load for an empty split (its lp_lo may be one past the last page).
     const uint32_t lp = c.lp_lo + lane;
-    c.ptab = lp <= c.lp_hi ? table[lp] : 0u;
+    c.ptab = s1 > s0 && lp <= c.lp_hi ? table[lp] : 0u;
   }
   // Issue sequence: this wave's tiles in order, the last one repeated past the
   // end (so every step issues exactly one tile).

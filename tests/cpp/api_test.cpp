@@ -68,6 +68,22 @@ int main() {
   expect(invalid_message([&] { kvbridge::merge_attention(base, fake, 255, fake, fake, fake, nullptr); }) !=
              "<no exception>",
          "merge split-count mismatch");
+  // batched extension: sizing and host-side rejections
+  const kvbridge::BatchShape bs{4, 1, 64, 8, 128, 64, 8192, 131072, 4 * 131072, 8192, 2048, 0.0883883f, true};
+  expect(kvbridge::batch_shape_error(bs) == nullptr, "valid batch shape");
+  expect(kvbridge::batch_split_count(bs) == 64, "batch split count");
+  expect(kvbridge::batch_scratch_elements(bs) == size_t(4) * 64 * 64 * 130, "batch scratch elements");
+  expect(kvbridge::batch_output_scalar_elements(bs) == 256, "batch output elements");
+  kvbridge::BatchShape bad_batch = bs;
+  bad_batch.batch = 0;
+  expect(invalid_message([&] { (void)kvbridge::batch_split_count(bad_batch); }) == "batch must be in [1,65535]",
+         "batch count message");
+  kvbridge::BatchInput bnone{};
+  expect(invalid_message([&] {
+           kvbridge::decode_attention_batched(bs, bnone, fake, nullptr, fake, fake, fake, nullptr,
+                                              kvbridge::OutputType::none, nullptr);
+         }) == "attention input device buffers must be non-null",
+         "batched null inputs message");
   if (failures) return 1;
   std::printf("PASS C++ API host checks\n");
   return 0;
