@@ -49,6 +49,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="skip the hipGraph replay (profiling runs)")
+    ap.add_argument("--no-five-layer", action="store_true", help="skip the five-layer graph step (configs[4])")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run known-size copy and read kernels (for scaling rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -206,6 +207,73 @@ def main():
     log(f"eager {eager_ms*1e3:.2f} us/call, graph {graph_ms*1e3 if graph_ms else float('nan'):.2f} us/call, "
         f"{split_kernel} {split_ms*1e3:.2f} us/launch ({split_gbs:.0f} GB/s), merge-only {merge_ms*1e3:.2f} us")
 
+    # ---- same-size streaming read: one launch reading the call's KV byte
+    # count with nothing else to do (rotated over as many buffers), the
+    # practical ceiling of any single launch that streams these bytes.
+    sink = torch.zeros(8192, dtype=torch.int32, device=dev)
+    probe_bufs = [torch.ones(kv_bytes, dtype=torch.uint8, device=dev) for _ in range(args.copies)]
+
+    def probe(i):
+        kvb.hbm_read_probe(probe_bufs[i % len(probe_bufs)], kv_bytes, sink, 2048, sp)
+
+    for i in range(args.warmup):
+        probe(i)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(args.steps):
+        probe(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    probe_us = e0.elapsed_time(e1) * 1e3 / args.steps
+    probe_gbs = kv_bytes / (probe_us * 1e-6) / 1e9
+    del probe_bufs
+    log(f"stream probe: {kv_bytes} B in {probe_us:.2f} us per launch ({probe_gbs:.0f} GB/s)")
+
+    # ---- five independent cfg2 layers, each one fused
+    # decode call, captured as one hipGraph step and replayed.
+    five = None
+    if not args.no_five_layer and not args.no_graph:
+        layers = list(range(min(5, len(caches))))
+        extra = []
+        while len(layers) + len(extra) < 5:
+            _, t_ = W.torch_cache(rows, qh, kvh, D, P, T, seed=0x4B56430 + len(extra), device="cuda:0")
+            extra.append(t_)
+        linps = [inps[i] for i in layers] + [kvb.device_input(t_["q"], t_["qpos"], t_["kpos"], t_["table"], t_["k"],
+                                                             t_["v"], t_["ks"], t_["vs"]) for t_ in extra]
+        lbufs = [dict(sc=torch.empty_like(scratch), cnt=torch.zeros(kvh, dtype=torch.int32, device=dev),
+                      m=torch.empty_like(m), l=torch.empty_like(l), n=torch.empty_like(n),
+                      o=torch.empty_like(out)) for _ in linps]
+        gs5 = torch.cuda.Stream()
+        gs5.wait_stream(stream)
+
+        def five_step(strm):
+            for li, b in zip(linps, lbufs):
+                kvb.decode_attention_fused(s, li, st, b["sc"], b["cnt"], b["m"], b["l"], b["n"], b["o"],
+                                           kvb.KVB_OUT_F16, strm)
+
+        with torch.cuda.stream(gs5):
+            five_step(gs5.cuda_stream)
+        torch.cuda.synchronize()
+        g5 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g5, stream=gs5):
+            five_step(gs5.cuda_stream)
+        for _ in range(5):
+            g5.replay()
+        torch.cuda.synchronize()
+        reps5 = max(10, args.steps // 5)
+        e0.record(stream)
+        for _ in range(reps5):
+            g5.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        step_us = e0.elapsed_time(e1) * 1e3 / reps5
+        five = {"layers": 5, "us_per_step": round(step_us, 3),
+                "GB/s": round(5 * kv_bytes / (step_us * 1e-6) / 1e9, 1),
+                "pct_of_peak": round(100.0 * 5 * kv_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
+                "kv_bytes_per_step": 5 * kv_bytes, "graph": True}
+        log(f"five-layer graph step: {step_us:.2f} us ({five['GB/s']:.0f} GB/s)")
+        del extra, lbufs
+
     # ---- known-size kernels for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE
     if args.calibrate:
         cal_bytes = 256 << 20
@@ -274,6 +342,10 @@ def main():
                      "kernel": fused_kernel, "algorithmic_bytes_per_launch": kv_bytes,
                      "launch_us": round(eager_ms * 1e3, 3)},
         "split_only": {"kernel": split_kernel, "us": round(split_ms * 1e3, 3), "GB/s": round(split_gbs, 1)},
+        "stream_probe": {"bytes": kv_bytes, "us": round(probe_us, 3), "GB/s": round(probe_gbs, 1),
+                         "pct_of_peak": round(100.0 * probe_gbs / HBM_PEAK_GBS, 2),
+                         "note": "one plain streaming-read launch of the call's KV byte count, rotated buffers"},
+        "five_layer_step": five,
         "cpu_baseline": cpu,
         "parity": parity,
     }
