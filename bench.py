@@ -211,10 +211,11 @@ def main():
     # count with nothing else to do (rotated over as many buffers), the
     # practical ceiling of any single launch that streams these bytes.
     sink = torch.zeros(8192, dtype=torch.int32, device=dev)
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count  # one work-group per CU
     probe_bufs = [torch.ones(kv_bytes, dtype=torch.uint8, device=dev) for _ in range(args.copies)]
 
     def probe(i):
-        kvb.hbm_read_probe(probe_bufs[i % len(probe_bufs)], kv_bytes, sink, 2048, sp)
+        kvb.hbm_read_probe(probe_bufs[i % len(probe_bufs)], kv_bytes, sink, n_cu, sp)
 
     for i in range(args.warmup):
         probe(i)
@@ -282,7 +283,7 @@ def main():
         sink = torch.zeros(8192, dtype=torch.int32, device=dev)
         for _ in range(5):
             dst.copy_(src)                                   # reads and writes cal_bytes
-            kvb.hbm_read_probe(src, cal_bytes, sink, 4096)   # reads cal_bytes
+            kvb.hbm_read_probe(src, cal_bytes, sink, n_cu)   # reads cal_bytes
         torch.cuda.synchronize()
         log(f"calibration: 5 x copy of {cal_bytes} B and 5 x read probe of {cal_bytes} B")
 

@@ -179,7 +179,8 @@ const char* kvb_selected_kernel_name(const kvb_shape* s, const kvb_device_input*
 
 /* Extension (diagnostic, no counterpart in the reference library): streams
  * `bytes` (a multiple of 16) of device memory with non-temporal 16-byte loads
- * over `blocks` work-groups of 256 threads, for measuring the device's
+ * over `blocks` work-groups of 512 threads (contiguous runs of 8 KiB items per
+ * work-group), for measuring the device's
  * achievable HBM read bandwidth next to the attention kernels (the role of the
  * reference's stream probe, data/att-bench-65536-v2-07.json:528-541).  `sink`
  * needs `blocks` uint32 and is practically never written. */

@@ -74,8 +74,9 @@ __device__ __forceinline__ uint32_t gload4(const float* p) {
 }
 
 // One item in registers: the K image (d[mb * D/64 + j] = 16 bytes of K row
-// 16*(m/4) + 4*mb + m%4, dims 64*j + 16*g ..) or the V image (d[mb] = V row
-// 16*mb + m, slots 16g .. 16g+15), plus k- and v-scale of token lane.
+// 16*(m/4) + 4*mb + m%4, dims 64*j + 16*g ..; with PAIR the half-row layout
+// below) plus k- and v-scale of token lane, or the V image (d[mb] = V row
+// 16*mb + m, slots 16g .. 16g+15), which reuses its tile's scales.
 template <int D>
 struct Slot {
   u32x4_t d[D / 16];
@@ -111,9 +112,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), kRsrcWord3);
 }
 
-// Issue one item (D/16 + 2 loads, unconditionally: an item past the wave's
-// last tile gets zero-sized descriptors, so its loads return 0 and move no
-// data).  PT: page_tokens is a power of two >= 64, the tile lies in one page
+// Issue one item (D/16 + 2 loads for K, D/16 for V, unconditionally: an
+// item past the wave's last tile gets zero-sized descriptors, so its loads
+// return 0 and move no data).  PT: page_tokens is a power of two >= 64, the tile lies in one page
 // and the descriptors are rebased on it (any pool size).  Otherwise
 // page_tokens is 16 or 32: every 16-token group lies in one page and lanes
 // address their group's page through whole-array descriptors.
@@ -145,8 +146,10 @@ __device__ __forceinline__ void issue_item(const IssueCtx& c, uint32_t tile, boo
 #pragma unroll
       for (uint32_t mb = 0; mb < D / 16; ++mb) s.d[mb] = bload16(r, c.voff_v, 16u * mb * c.P);
     }
-    s.ks = bload4(rsrc(c.ks + tok, real ? 256u : 0u), c.voff_s, 0u);
-    s.vs = bload4(rsrc(c.vs + tok, real ? 256u : 0u), c.voff_s, 0u);
+    if constexpr (!IS_V) {  // the tile's V item reuses these
+      s.ks = bload4(rsrc(c.ks + tok, real ? 256u : 0u), c.voff_s, 0u);
+      s.vs = bload4(rsrc(c.vs + tok, real ? 256u : 0u), c.voff_s, 0u);
+    }
   } else {
     const uint32_t lane = c.lane, m = lane & 15u, g = lane >> 4;
     uint32_t slab[4];  // slab of token group q (tokens t0+16q ..), uniform
@@ -182,9 +185,11 @@ __device__ __forceinline__ void issue_item(const IssueCtx& c, uint32_t tile, boo
 #pragma unroll
       for (uint32_t mb = 0; mb < D / 16; ++mb) s.d[mb] = bload16(r, voff, 16u * mb * c.P);
     }
-    const uint32_t si = (pick(g) * c.P + ((t0 + 16u * g) & (c.P - 1u)) + m) * 4u;
-    s.ks = bload4(real ? c.rks : none, si, 0u);
-    s.vs = bload4(real ? c.rvs : none, si, 0u);
+    if constexpr (!IS_V) {  // the tile's V item reuses these
+      const uint32_t si = (pick(g) * c.P + ((t0 + 16u * g) & (c.P - 1u)) + m) * 4u;
+      s.ks = bload4(real ? c.rks : none, si, 0u);
+      s.vs = bload4(real ? c.rvs : none, si, 0u);
+    }
   }
 }
 
@@ -566,6 +571,7 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
   // State.  Lane-as-token view: sc, mx, lw, lrun per head-row.  MFMA view:
   // int32 digit numerators acc_i, fp32 numerators acc_f (head = lane & 15).
   float sc[kChunk][HS];
+  float vsc[kChunk];  // v-scale of token lane, per tile of the chunk
   float mx[HS], lw[HS], lrun[HS];
   float m_run[HS], m_new[HS], mu[HS];
   float vmx = 0.f;
@@ -641,6 +647,7 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
     });
     const float ks_l = __uint_as_float(it.ks);
     const float vs_l = __uint_as_float(it.vs);
+    vsc[r] = vs_l;  // for the tile's V item (which loads no scales)
     vmx = fmaxf(vmx, tok_ok ? fabsf(vs_l) : 0.f);
 #pragma unroll
     for (int h = 0; h < HS; ++h) {
@@ -660,7 +667,7 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
     const uint32_t tok = t0 + lane;
     const bool real = i < nt;
     const bool tok_ok = real && ((t0 >= s0 && t0 + kTileTokens <= e_min) || (tok >= s0 && tok < e_max));
-    const float vs_l = tok_ok ? __uint_as_float(it.vs) : 0.f;
+    const float vs_l = tok_ok ? vsc[r] : 0.f;
     static_for<0, HS>([&](auto hc) __attribute__((always_inline)) {
       constexpr uint32_t h = decltype(hc)::value;
       const float w = __builtin_amdgcn_exp2f(sc[r][h] - mu[h]);  // w * 2^kp
