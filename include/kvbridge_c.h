@@ -167,6 +167,39 @@ int kvb_decode_attention_batched(const kvb_batch_shape* s, const kvb_batch_input
  * would launch ("" if the arguments are invalid). */
 const char* kvb_batch_kernel_name(const kvb_batch_shape* s, const kvb_batch_input* in, int fused);
 
+/* Extension (no counterpart in the reference library, which ships no cache
+ * writer; the write side of the layout in include/kvbridge/attention_common.h
+ * and of the quantization the decode configs use): quantize the K and V rows
+ * of `tokens` new tokens and store them into the paged pool.  New token t,
+ * kv head h: its rows k_new[t * k_stride + h * dim + d] (likewise v_new) in
+ * src_type (KVB_SRC_*) go to physical slot slots[t] (page = slot /
+ * page_tokens), with per-(token, kv head) scale = absmax / 127 (1 when the
+ * row is all zero) and code = clamp(rint(x / scale), -127, 127) in IEEE fp32
+ * (round to nearest even): K token-major, V dim-major, scales into
+ * k_scales / v_scales.  slots is a device array; ids >= pages * page_tokens
+ * are skipped (padding).  Two tokens with the same slot race.  Asynchronous
+ * on `stream`, allocates nothing. */
+enum { KVB_SRC_F32 = 1, KVB_SRC_F16 = 2, KVB_SRC_BF16 = 3 };
+typedef struct kvb_append_shape {
+  uint32_t tokens, kv_heads, dim, page_tokens, pages;
+  uint32_t k_stride, v_stride; /* elements between consecutive new tokens */
+  uint32_t src_type;
+} kvb_append_shape;
+
+typedef struct kvb_append_io {
+  const void* k_new;
+  const void* v_new;
+  const uint32_t* slots;
+  int8_t* k;
+  int8_t* v;
+  float* k_scales;
+  float* v_scales;
+} kvb_append_io;
+
+/* NULL when valid, else the first failed rule's message. */
+const char* kvb_append_shape_error(const kvb_append_shape* s);
+int kvb_append_kv(const kvb_append_shape* s, const kvb_append_io* io, void* stream);
+
 /* Extension (diagnostic): which split kernel kvb_split_attention would run for
  * these arguments: KVB_KERNEL_TILED_MFMA or KVB_KERNEL_GENERIC; 0 if invalid. */
 int kvb_selected_kernel(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens);

@@ -13,6 +13,11 @@ from __future__ import annotations
 import ctypes
 
 from ._capi import (  # noqa: F401
+    KVB_SRC_BF16,
+    KVB_SRC_F16,
+    KVB_SRC_F32,
+    AppendIO,
+    AppendShape,
     BatchInput,
     BatchShape,
     KVB_KERNEL_GENERIC,
@@ -221,3 +226,25 @@ def decode_attention_batched(s: BatchShape, inp: BatchInput, scratch, m, l, n, o
 
 def batch_kernel_name(s: BatchShape, inp: BatchInput, fused: bool = False) -> str:
     return load().kvb_batch_kernel_name(ctypes.byref(s), ctypes.byref(inp), int(fused)).decode()
+
+
+# ---- paged INT8 KV append (kvb_append_kv) ---------------------------------------
+
+def append_shape(tokens, kv_heads, dim, page_tokens, pages, src_type=KVB_SRC_F32, k_stride=None,
+                 v_stride=None) -> AppendShape:
+    row = kv_heads * dim
+    return AppendShape(tokens, kv_heads, dim, page_tokens, pages, row if k_stride is None else k_stride,
+                       row if v_stride is None else v_stride, src_type)
+
+
+def append_shape_error(s: AppendShape):
+    r = load().kvb_append_shape_error(ctypes.byref(s))
+    return None if r is None else r.decode()
+
+
+def append_kv(s: AppendShape, k_new, v_new, slots, k, v, k_scales, v_scales, stream=None) -> None:
+    """Quantize new tokens' K/V rows into their physical slots of the pool
+    (kvb_append_kv): per-(token, kv head) absmax scales, K token-major, V
+    dim-major."""
+    io = AppendIO(*(_ptr(x) for x in (k_new, v_new, slots, k, v, k_scales, v_scales)))
+    check(load().kvb_append_kv(ctypes.byref(s), ctypes.byref(io), _stream(stream)))

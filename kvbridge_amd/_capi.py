@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 KVB_OK, KVB_EINVAL, KVB_ERUNTIME = 0, 1, 2
 KVB_OUT_NONE, KVB_OUT_F32, KVB_OUT_F16 = 0, 1, 2
 KVB_KERNEL_TILED_MFMA, KVB_KERNEL_GENERIC = 1, 2
+KVB_SRC_F32, KVB_SRC_F16, KVB_SRC_BF16 = 1, 2, 3
 
 
 class Shape(ctypes.Structure):
@@ -83,6 +84,19 @@ class BatchInput(ctypes.Structure):
                  "k", "v", "k_scales", "v_scales")]
 
 
+class AppendShape(ctypes.Structure):
+    """kvb_append_shape (include/kvbridge_c.h)."""
+
+    _fields_ = [(n, ctypes.c_uint32) for n in
+                ("tokens", "kv_heads", "dim", "page_tokens", "pages", "k_stride", "v_stride", "src_type")]
+
+
+class AppendIO(ctypes.Structure):
+    """kvb_append_io (include/kvbridge_c.h)."""
+
+    _fields_ = [(n, ctypes.c_void_p) for n in ("k_new", "v_new", "slots", "k", "v", "k_scales", "v_scales")]
+
+
 class KvbError(Exception):
     """Base class; the subclasses mirror std::invalid_argument / std::runtime_error."""
 
@@ -134,6 +148,8 @@ SIGNATURES = [
     ("kvb_batch_output_scalar_elements", _INT, [_BSP, ctypes.POINTER(ctypes.c_size_t)]),
     ("kvb_decode_attention_batched", _INT, [_BSP, _BIP, _VP, _VP, _VP, _VP, _VP, _VP, _INT, _VP]),
     ("kvb_batch_kernel_name", ctypes.c_char_p, [_BSP, _BIP, _INT]),
+    ("kvb_append_shape_error", ctypes.c_char_p, [ctypes.POINTER(AppendShape)]),
+    ("kvb_append_kv", _INT, [ctypes.POINTER(AppendShape), ctypes.POINTER(AppendIO), _VP]),
 ]
 
 _lib = None

@@ -262,6 +262,7 @@ int kvb_preload_attention_reference_kernels(void) {
   if (e == hipSuccess) e = kvb::preload_i8();
   if (e == hipSuccess) e = kvb::preload_lds();
   if (e == hipSuccess) e = kvb::preload_merge();
+  if (e == hipSuccess) e = kvb::preload_append();
   return int(e);
 }
 
@@ -527,6 +528,50 @@ const char* kvb_batch_kernel_name(const kvb_batch_shape* sp, const kvb_batch_inp
   static uint32_t dummy_counter;  // only its non-nullness is read
   if (fused && i8) a.counters = &dummy_counter;
   return kvb::split_kernel_name(a, i8, b.int8);
+}
+
+const char* kvb_append_shape_error(const kvb_append_shape* s) {
+  if (!s) return "shape pointer must be non-null";
+  if (s->kv_heads == 0 || s->page_tokens == 0 || s->pages == 0)
+    return "kv_heads, page_tokens and pages must be positive";
+  if (s->dim < 1 || s->dim > 256) return "dim must be in [1,256]";
+  const uint64_t extent = uint64_t(s->pages) * s->kv_heads * s->page_tokens * s->dim;
+  if (extent > 0xffffffffull) return "physical KV extent exceeds 32-bit kernel offsets";
+  if (s->src_type != KVB_SRC_F32 && s->src_type != KVB_SRC_F16 && s->src_type != KVB_SRC_BF16)
+    return "unknown source element type";
+  if (uint64_t(s->k_stride) < uint64_t(s->kv_heads) * s->dim || uint64_t(s->v_stride) < uint64_t(s->kv_heads) * s->dim)
+    return "token stride must cover kv_heads * dim elements";
+  return nullptr;
+}
+
+int kvb_append_kv(const kvb_append_shape* s, const kvb_append_io* io, void* stream) {
+  return guarded([&]() -> int {
+    if (!s || !io) return fail(KVB_EINVAL, "shape and buffer descriptors must be non-null");
+    if (const char* e = kvb_append_shape_error(s)) return fail(KVB_EINVAL, e);
+    if (s->tokens == 0) return KVB_OK;
+    if (!io->k_new || !io->v_new || !io->slots || !io->k || !io->v || !io->k_scales || !io->v_scales)
+      return fail(KVB_EINVAL, "append buffers must be non-null");
+    const uintptr_t el = s->src_type == KVB_SRC_F32 ? 4 : 2;
+    if (reinterpret_cast<uintptr_t>(io->k_new) % el || reinterpret_cast<uintptr_t>(io->v_new) % el)
+      return fail(KVB_EINVAL, "source rows must be aligned to their element size");
+    kvb::AppendArgs a{};
+    a.k_new = io->k_new;
+    a.v_new = io->v_new;
+    a.slots = io->slots;
+    a.k = io->k;
+    a.v = io->v;
+    a.k_scales = io->k_scales;
+    a.v_scales = io->v_scales;
+    a.tokens = s->tokens;
+    a.kv_heads = s->kv_heads;
+    a.dim = s->dim;
+    a.page_tokens = s->page_tokens;
+    a.pages = s->pages;
+    a.k_stride = s->k_stride;
+    a.v_stride = s->v_stride;
+    a.src_type = int(s->src_type);
+    return hip_status(kvb::launch_append(a, static_cast<hipStream_t>(stream)), "kv append launch");
+  });
 }
 
 }  // extern "C"

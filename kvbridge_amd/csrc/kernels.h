@@ -71,6 +71,25 @@ hipError_t launch_merge(uint32_t row_heads, uint32_t dim, uint32_t splits, const
                         float* m, float* l, float* n, void* out, int out_type,
                         hipStream_t stream);
 
+// Paged INT8 KV append (append.hip): tokens rows of k_new / v_new
+// ([token][kv_head][dim] at k_stride / v_stride elements per token, element
+// type src_type: 1 fp32, 2 fp16, 3 bf16) quantized into physical slots
+// slots[t] (page = slot / page_tokens) of the pool.
+struct AppendArgs {
+  const void* k_new;
+  const void* v_new;
+  const uint32_t* slots;
+  int8_t* k;
+  int8_t* v;
+  float* k_scales;
+  float* v_scales;
+  uint32_t tokens, kv_heads, dim, page_tokens, pages;
+  uint32_t k_stride, v_stride;
+  int src_type;
+};
+hipError_t launch_append(const AppendArgs& a, hipStream_t stream);
+hipError_t preload_append();
+
 // Streaming HBM read probe (diagnostic).
 hipError_t launch_read_probe(const void* src, size_t bytes, uint32_t* sink, uint32_t blocks,
                              hipStream_t stream);

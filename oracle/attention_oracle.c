@@ -13,6 +13,10 @@
  *                       with l <= 0 skipped)
  *   oracle_fixture      examples/attention_reference.h:19-48 (closed-form
  *                       patterned fixture)
+ *   oracle_append_int8  the per-(token, kv head) symmetric int8 quantization
+ *                       BASELINE.json's configs describe (the reference ships
+ *                       no cache writer), stored in the reference's layout
+ *                       (include/kvbridge/attention_common.h:11-46)
  * Pinned by tests/test_oracle.py against the reference's own known-answer
  * tests (tests/reference_test.cpp), golden vectors produced by the
  * reference's FP64 oracle built from source (tests/golden), and closed forms.
@@ -302,6 +306,49 @@ void oracle_fixture(uint32_t tokens, int permute, float* q, int64_t* qpos, int64
         v[(((size_t)page * kv_heads + h) * dim + d) * P + slot] =
             (int8_t)((int)((t * 7 + h * 13 + d * 5) % 256) - 128);
       }
+    }
+  }
+}
+
+static void quantize_row(const float* x, uint32_t dim, int8_t* code, float* scale) {
+  float amax = 0.0f;
+  for (uint32_t d = 0; d < dim; ++d) {
+    const float a = fabsf(x[d]);
+    if (a > amax) amax = a;
+  }
+  const float div = g_fault == ORACLE_FAULT_QUANT_SCALE_128 ? 128.0f : 127.0f;
+  const float sc = amax == 0.0f ? 1.0f : amax / div;
+  for (uint32_t d = 0; d < dim; ++d) {
+    const float q = x[d] / sc;
+    float r = g_fault == ORACLE_FAULT_QUANT_ROUND_AWAY ? roundf(q) : rintf(q);
+    if (r > 127.0f) r = 127.0f;
+    if (r < -127.0f) r = -127.0f;
+    code[d] = (int8_t)r;
+  }
+  *scale = sc;
+}
+
+void oracle_append_int8(uint32_t tokens, uint32_t kv_heads, uint32_t dim, uint32_t page_tokens, uint32_t pages,
+                        const float* k_new, const float* v_new, uint32_t k_stride, uint32_t v_stride,
+                        const uint32_t* slots, int8_t* k, int8_t* v, float* ks, float* vs) {
+  int8_t code[256];
+  for (uint32_t t = 0; t < tokens; ++t) {
+    const uint32_t id = slots[t];
+    if ((uint64_t)id >= (uint64_t)pages * page_tokens) continue;
+    const size_t page = id / page_tokens, slot = id % page_tokens;
+    for (uint32_t h = 0; h < kv_heads; ++h) {
+      const size_t row = (page * kv_heads + h) * page_tokens + slot;
+      float sc;
+      quantize_row(k_new + (size_t)t * k_stride + (size_t)h * dim, dim, code, &sc);
+      memcpy(k + row * dim, code, dim);
+      ks[row] = sc;
+      quantize_row(v_new + (size_t)t * v_stride + (size_t)h * dim, dim, code, &sc);
+      for (uint32_t d = 0; d < dim; ++d) {
+        const size_t vi = g_fault == ORACLE_FAULT_QUANT_V_TOKEN_MAJOR ? row * dim + d
+                                                                       : ((page * kv_heads + h) * dim + d) * page_tokens + slot;
+        v[vi] = code[d];
+      }
+      vs[row] = sc;
     }
   }
 }

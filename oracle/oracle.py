@@ -52,6 +52,9 @@ FAULTS = {
     "gqa_modulo": 7,
     "split_ignores_begin": 8,
     "merge_no_skip": 9,
+    "quant_round_away": 10,
+    "quant_scale_128": 11,
+    "quant_v_token_major": 12,
 }
 
 
@@ -186,3 +189,21 @@ def gates(actual: np.ndarray, ref: np.ndarray):
     rel_l2 = float(np.linalg.norm(a - r) / denom) if denom > 0 else float(np.linalg.norm(a - r))
     strict = bool(np.all(err <= 3e-6 + 5e-5 * np.abs(r)))
     return {"max_abs": max_abs, "rel_l2": rel_l2, "pass": max_abs <= 2e-3 and rel_l2 <= 1e-3, "strict_pass": strict}
+
+
+def append_int8(pool_k, pool_v, pool_ks, pool_vs, k_new, v_new, slots, page_tokens):
+    """Quantizing append into copies of the pool arrays (oracle_append_int8).
+    pool_k int8 [pages, kv, P, D], pool_v int8 [pages, kv, D, P], scales [pages, kv, P];
+    k_new / v_new float32 [tokens, kv, D]; slots uint32 [tokens]."""
+    k, v = np.array(pool_k, np.int8, copy=True), np.array(pool_v, np.int8, copy=True)
+    ks, vs = np.array(pool_ks, np.float32, copy=True), np.array(pool_vs, np.float32, copy=True)
+    kn = np.ascontiguousarray(k_new, np.float32)
+    vn = np.ascontiguousarray(v_new, np.float32)
+    sl = np.ascontiguousarray(slots, np.uint32)
+    tokens, kvh, dim = kn.shape
+    pages = k.shape[0]
+    lib().oracle_append_int8(ctypes.c_uint32(tokens), ctypes.c_uint32(kvh), ctypes.c_uint32(dim),
+                             ctypes.c_uint32(page_tokens), ctypes.c_uint32(pages), _p(kn), _p(vn),
+                             ctypes.c_uint32(kvh * dim), ctypes.c_uint32(kvh * dim), _p(sl), _p(k), _p(v), _p(ks),
+                             _p(vs))
+    return k, v, ks, vs

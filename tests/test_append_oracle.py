@@ -1,0 +1,85 @@
+"""CPU checks of the quantizing append restatement (oracle_append_int8):
+known answers (ties round to even, all-zero rows get scale 1, +-absmax maps
+to +-127), an independent numpy formulation (the synthetic-data quantizer,
+scattered into the page layout) on random and tie-heavy rows, padding slots,
+and planted mistakes that these checks must catch."""
+import numpy as np
+import pytest
+
+from kvbridge_amd import workloads as W
+from oracle import oracle as O
+
+
+def empty_pool(pages, kvh, P, D):
+    rng = np.random.default_rng(0)
+    k = rng.integers(-128, 128, (pages, kvh, P, D), dtype=np.int8)
+    v = rng.integers(-128, 128, (pages, kvh, D, P), dtype=np.int8)
+    ks = rng.random((pages, kvh, P), dtype=np.float32)
+    vs = rng.random((pages, kvh, P), dtype=np.float32)
+    return k, v, ks, vs
+
+
+def numpy_append(pool, kn, vn, slots, P):
+    """Independent formulation: quantize_rows per (token, kv head), then scatter."""
+    k, v, ks, vs = (np.array(a, copy=True) for a in pool)
+    kc, kscale = W.quantize_rows(kn)
+    vc, vscale = W.quantize_rows(vn)
+    pages = k.shape[0]
+    for t, sid in enumerate(slots):
+        if sid >= pages * P:
+            continue
+        page, slot = divmod(int(sid), P)
+        k[page, :, slot, :] = kc[t]
+        v[page, :, :, slot] = vc[t]
+        ks[page, :, slot] = kscale[t]
+        vs[page, :, slot] = vscale[t]
+    return k, v, ks, vs
+
+
+def test_known_answers():
+    pool = empty_pool(2, 1, 4, 3)
+    kn = np.array([[[127., 0.5, -1.5]], [[0, 0, 0]]], np.float32)
+    vn = np.array([[[2.5, -2.5, 127]], [[1, 2, 3]]], np.float32)
+    k, v, ks, vs = O.append_int8(*pool, kn, vn, np.array([5, 1], np.uint32), 4)
+    assert k[1, 0, 1].tolist() == [127, 0, -2] and ks[1, 0, 1] == 1.0
+    assert v[1, 0, :, 1].tolist() == [2, -2, 127] and vs[1, 0, 1] == 1.0
+    assert k[0, 0, 1].tolist() == [0, 0, 0] and ks[0, 0, 1] == 1.0
+    assert v[0, 0, :, 1].tolist() == [42, 85, 127] and vs[0, 0, 1] == np.float32(3) / np.float32(127)
+    # untouched slots keep their contents
+    assert np.array_equal(k[0, 0, 0], pool[0][0, 0, 0]) and v[0, 0, 0, 0] == pool[1][0, 0, 0, 0]
+
+
+@pytest.mark.parametrize("D,kvh,P,tokens", [(128, 8, 64, 200), (64, 2, 16, 97), (67, 3, 32, 50), (256, 1, 64, 33)])
+def test_matches_numpy_formulation(D, kvh, P, tokens):
+    rng = np.random.default_rng(D * 1000 + tokens)
+    pages = -(-tokens // P) + 2
+    pool = empty_pool(pages, kvh, P, D)
+    kn = rng.standard_normal((tokens, kvh, D), dtype=np.float32)
+    vn = rng.standard_normal((tokens, kvh, D), dtype=np.float32) * 3
+    kn[0, 0] = 0.0                                    # all-zero row
+    vn[1, :, :] = np.round(vn[1] * 2) / 2             # many exact halves after scaling by 1
+    vn[1, :, 0] = 127.0                               # absmax 127 -> scale exactly 1 -> ties at .5
+    slots = rng.permutation(pages * P)[:tokens].astype(np.uint32)
+    slots[3] = 0xFFFFFFFF                             # padding entry: skipped
+    got = O.append_int8(*pool, kn, vn, slots, P)
+    want = numpy_append(pool, kn, vn, slots, P)
+    for g, w in zip(got, want):
+        assert np.array_equal(g, w)
+
+
+@pytest.mark.parametrize("fault", ["quant_round_away", "quant_scale_128", "quant_v_token_major"])
+def test_planted_mistakes_are_caught(fault):
+    rng = np.random.default_rng(5)
+    P, D, kvh, tokens = 16, 64, 2, 40
+    pool = empty_pool(4, kvh, P, D)
+    kn = rng.standard_normal((tokens, kvh, D), dtype=np.float32)
+    vn = np.round(rng.standard_normal((tokens, kvh, D), dtype=np.float32) * 8) / 2
+    vn[:, :, 0] = 127.0
+    slots = rng.permutation(4 * P)[:tokens].astype(np.uint32)
+    want = numpy_append(pool, kn, vn, slots, P)
+    O.set_fault(O.FAULTS[fault])
+    try:
+        got = O.append_int8(*pool, kn, vn, slots, P)
+    finally:
+        O.set_fault(0)
+    assert not all(np.array_equal(g, w) for g, w in zip(got, want)), fault

@@ -1,0 +1,126 @@
+"""Paged INT8 KV append (kvb_append_kv) on the GPU: codes and scales are
+bitwise those of the CPU restatement (oracle_append_int8) for fp32, fp16 and
+bf16 sources, strided sources, padding slots and odd head dims, untouched
+slots keep their bytes; and a cache written token by token through the
+append path is bitwise the cache the synthetic generator builds, and decodes
+to the FP64 oracle's output."""
+import numpy as np
+import pytest
+
+import kvbridge_amd as kvb
+from kvbridge_amd import workloads as W
+from oracle import oracle as O
+
+from helpers import DeviceCase, check_against_oracle, log
+
+pytestmark = pytest.mark.gpu
+
+SRC = {kvb.KVB_SRC_F32: "float32", kvb.KVB_SRC_F16: "float16", kvb.KVB_SRC_BF16: "bfloat16"}
+
+
+def random_pool(pages, kvh, P, D, seed):
+    rng = np.random.default_rng(seed)
+    return (rng.integers(-128, 128, (pages, kvh, P, D), dtype=np.int8),
+            rng.integers(-128, 128, (pages, kvh, D, P), dtype=np.int8),
+            rng.random((pages, kvh, P), dtype=np.float32), rng.random((pages, kvh, P), dtype=np.float32))
+
+
+CASES = [
+    # tokens, kv_heads, dim, page, src, extra stride (elements)
+    (300, 8, 128, 64, kvb.KVB_SRC_F32, 0),
+    (77, 8, 128, 64, kvb.KVB_SRC_F16, 0),
+    (129, 2, 64, 16, kvb.KVB_SRC_BF16, 0),
+    (50, 3, 67, 32, kvb.KVB_SRC_F32, 0),
+    (40, 1, 256, 64, kvb.KVB_SRC_F16, 0),
+    (64, 8, 128, 64, kvb.KVB_SRC_BF16, 4096),   # rows inside a wider (fused QKV-like) buffer
+    (1, 8, 128, 64, kvb.KVB_SRC_F32, 0),        # one decode-step token
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_append_matches_oracle_bitwise(gpu, case):
+    import torch
+
+    tokens, kvh, D, P, src, extra = case
+    rng = np.random.default_rng(tokens * 31 + D)
+    pages = -(-tokens // P) + 3
+    pool = random_pool(pages, kvh, P, D, seed=tokens)
+    row = kvh * D
+    stride = row + extra
+    tdt = getattr(torch, SRC[src])
+    kbuf = torch.from_numpy(rng.standard_normal((tokens, stride), dtype=np.float32) * 2).to(tdt)
+    vbuf = torch.from_numpy(rng.standard_normal((tokens, stride), dtype=np.float32) * 0.5).to(tdt)
+    kbuf[0, :D] = 0                                   # an all-zero row
+    vbuf[-1, :D] = torch.tensor(np.round(rng.standard_normal(D) * 4) / 2, dtype=tdt)  # exact halves
+    vbuf[-1, 0] = 127
+    slots = rng.permutation(pages * P)[:tokens].astype(np.uint32)
+    if tokens > 3:
+        slots[2] = 0xFFFFFFFF                         # padding entry
+    # host reference on the exactly representable fp32 values of the source
+    kn = kbuf.float().numpy()[:, :row].reshape(tokens, kvh, D)
+    vn = vbuf.float().numpy()[:, :row].reshape(tokens, kvh, D)
+    want = O.append_int8(*pool, kn, vn, slots, P)
+    dev = [torch.from_numpy(np.ascontiguousarray(a)).to(gpu) for a in pool]
+    s = kvb.append_shape(tokens, kvh, D, P, pages, src, stride, stride)
+    log(f"append tokens={tokens} kv={kvh} dim={D} page={P} src={SRC[src]} stride={stride}")
+    kvb.append_kv(s, kbuf.to(gpu), vbuf.to(gpu), torch.from_numpy(slots.view(np.int32)).to(gpu), *dev)
+    torch.cuda.synchronize()
+    for name, g, w in zip(("k", "v", "k_scales", "v_scales"), dev, want):
+        got = g.cpu().numpy()
+        assert np.array_equal(got.view(np.uint8) if got.dtype == np.int8 else got.view(np.uint32),
+                              w.view(np.uint8) if w.dtype == np.int8 else w.view(np.uint32)), f"{name} differs"
+
+
+def test_cache_written_by_append_decodes(gpu):
+    """Prefill a cfg2-shaped (shorter) cache through three append calls; it
+    equals the synthetic generator's cache bitwise and decodes to FP64."""
+    import torch
+
+    T, kvh, D, P, qh = 8192, 8, 128, 64, 32
+    case = W.synth_case(1, qh, kvh, D, P, T, seed=123)
+    pages = case.shape.pages
+    # recover the fp32 source rows of the generator (same seed, same draws)
+    rng = np.random.default_rng(123)
+    _q = rng.standard_normal(qh * D, dtype=np.float32)
+    kx = rng.standard_normal((pages, kvh, P, D), dtype=np.float32)
+    vx = rng.standard_normal((pages, kvh, P, D), dtype=np.float32)
+    # logical token t lives in physical page table[t // P], slot t % P; the
+    # generator drew rows per physical (page, kv, slot)
+    table = case.table.astype(np.int64)
+    t = np.arange(T)
+    phys = table[t // P]
+    kn = kx[phys, :, t % P, :]                       # [T, kv, D]
+    vn = vx[phys, :, t % P, :]
+    slots = (phys * P + t % P).astype(np.uint32)
+    dev_k = torch.zeros(case.k.shape, dtype=torch.int8, device=gpu)
+    dev_v = torch.zeros(case.v.shape, dtype=torch.int8, device=gpu)
+    dev_ks = torch.zeros(case.ks.shape, dtype=torch.float32, device=gpu)
+    dev_vs = torch.zeros(case.vs.shape, dtype=torch.float32, device=gpu)
+    kn_d = torch.from_numpy(np.ascontiguousarray(kn)).to(gpu)
+    vn_d = torch.from_numpy(np.ascontiguousarray(vn)).to(gpu)
+    sl_d = torch.from_numpy(slots.view(np.int32)).to(gpu)
+    for lo, hi in ((0, 1000), (1000, 1001), (1001, T)):   # prefill chunks incl. a single-token step
+        s = kvb.append_shape(hi - lo, kvh, D, P, pages)
+        kvb.append_kv(s, kn_d[lo:hi], vn_d[lo:hi], sl_d[lo:hi], dev_k, dev_v, dev_ks, dev_vs)
+    torch.cuda.synchronize()
+    assert np.array_equal(dev_k.cpu().numpy(), case.k), "K pool differs from the generator's"
+    assert np.array_equal(dev_v.cpu().numpy(), case.v), "V pool differs from the generator's"
+    assert np.array_equal(dev_ks.cpu().numpy(), case.ks) and np.array_equal(dev_vs.cpu().numpy(), case.vs)
+    dc = DeviceCase(case)
+    dc.t.update(k=dev_k, v=dev_v, ks=dev_ks, vs=dev_vs)
+    dc.inp = kvb.device_input(dc.t["q"], dc.t["qpos"], dc.t["kpos"], dc.t["table"], dev_k, dev_v, dev_ks, dev_vs)
+    mln, _, _ = dc.run_decode(2048)
+    check_against_oracle(case, mln, "decode of the appended cache")
+
+
+def test_append_rejections(gpu):
+    import torch
+
+    s = kvb.append_shape(4, 8, 128, 64, 10)
+    buf = torch.zeros(4 * 8 * 128, dtype=torch.float32, device=gpu)
+    sl = torch.zeros(4, dtype=torch.int32, device=gpu)
+    with pytest.raises(kvb.KvbInvalidArgument, match="non-null"):
+        kvb.append_kv(s, buf, buf, sl, None, buf, buf, buf)
+    with pytest.raises(kvb.KvbInvalidArgument, match="stride"):
+        kvb.append_kv(kvb.append_shape(4, 8, 128, 64, 10, k_stride=100), buf, buf, sl, buf, buf, buf, buf)
+    kvb.append_kv(kvb.append_shape(0, 8, 128, 64, 10), None, None, None, None, None, None, None)  # no-op
