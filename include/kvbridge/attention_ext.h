@@ -88,4 +88,24 @@ void decode_attention_batched(const BatchShape&, const BatchInput&, float* scrat
                               uint32_t* counters, float* m, float* l, float* n, void* out,
                               OutputType out_type, hipStream_t stream);
 
+// ---- paged INT8 KV append: the write side of the cache layout.
+// New token t, kv head h: the rows k_new / v_new[t * stride + h * dim + d]
+// (fp32, fp16 or bf16) are quantized with scale = absmax / 127 (1 for an
+// all-zero row) and code = clamp(rint(x / scale), -127, 127) in IEEE fp32,
+// and stored at physical slot slots[t] (page = slot / page_tokens): K
+// token-major, V dim-major, scales per (page, kv head, slot).  slots is a
+// device array; ids >= pages * page_tokens are skipped.
+enum class SourceType : int { f32 = 1, f16 = 2, bf16 = 3 };
+
+struct AppendShape {
+  unsigned tokens, kv_heads, dim, page_tokens, pages;
+  unsigned k_stride, v_stride;  // elements between consecutive new tokens (>= kv_heads * dim)
+  SourceType src_type;
+};
+
+// Throws std::invalid_argument for an invalid shape or null buffers,
+// std::runtime_error for a launch failure.  Asynchronous on `stream`.
+void append_kv(const AppendShape&, const void* k_new, const void* v_new, const uint32_t* slots, int8_t* k,
+               int8_t* v, float* k_scales, float* v_scales, hipStream_t stream);
+
 }  // namespace kvbridge

@@ -86,4 +86,12 @@ void decode_attention_batched(const BatchShape& b, const BatchInput& in, float* 
   check(kvb_decode_attention_batched(&cs, &ci, scratch, counters, m, l, n, out, int(out_type), stream));
 }
 
+void append_kv(const AppendShape& a, const void* k_new, const void* v_new, const uint32_t* slots, int8_t* k,
+               int8_t* v, float* k_scales, float* v_scales, hipStream_t stream) {
+  const kvb_append_shape cs{a.tokens,   a.kv_heads, a.dim,      a.page_tokens,
+                            a.pages,    a.k_stride, a.v_stride, uint32_t(a.src_type)};
+  const kvb_append_io io{k_new, v_new, slots, k, v, k_scales, v_scales};
+  check(kvb_append_kv(&cs, &io, stream));
+}
+
 }  // namespace kvbridge

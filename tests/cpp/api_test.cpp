@@ -84,6 +84,17 @@ int main() {
                                               kvbridge::OutputType::none, nullptr);
          }) == "attention input device buffers must be non-null",
          "batched null inputs message");
+  // append extension: host-side rejections
+  const kvbridge::AppendShape as{4, 8, 128, 64, 10, 1024, 1024, kvbridge::SourceType::f16};
+  expect(invalid_message([&] {
+           kvbridge::append_kv(as, fake, fake, nullptr, nullptr, nullptr, fake, fake, nullptr);
+         }) == "append buffers must be non-null",
+         "append null buffers message");
+  kvbridge::AppendShape as_bad = as;
+  as_bad.dim = 0;
+  expect(invalid_message([&] { kvbridge::append_kv(as_bad, fake, fake, nullptr, nullptr, nullptr, fake, fake, nullptr); }) ==
+             "dim must be in [1,256]",
+         "append dim message");
   if (failures) return 1;
   std::printf("PASS C++ API host checks\n");
   return 0;
