@@ -223,6 +223,7 @@ def test_batched_graph_replay_with_changing_lengths(gpu):
     out = torch.zeros(db.rh * 128, dtype=torch.float16, device=gpu)
     stream = torch.cuda.Stream()
     g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()  # `out` was filled on the default stream
     with torch.cuda.stream(stream):  # warm-up on the capture stream
         kvb.decode_attention_batched(bc.shape, db.inp, db.scratch, db.m, db.l, db.n, out, kvb.KVB_OUT_F16,
                                      counters=db.counters, stream=stream.cuda_stream)

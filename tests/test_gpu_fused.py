@@ -91,6 +91,7 @@ def test_fused_back_to_back_and_graph(gpu):
     outs = [torch.zeros(32 * 128, dtype=torch.float16, device=gpu) for _ in dcs]
     g = torch.cuda.CUDAGraph()
     stream = torch.cuda.Stream()
+    torch.cuda.synchronize()  # buffers above were filled on the default stream
     with torch.cuda.stream(stream):
         for dc, sc, o in zip(dcs, scs, outs):
             kvb.decode_attention_fused(s, dc.inp, st, sc, counters, dc.m, dc.l, dc.n, o, kvb.KVB_OUT_F16,

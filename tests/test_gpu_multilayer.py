@@ -36,6 +36,7 @@ def test_five_layer_graph_step(gpu):
             out=torch.zeros(32 * 128, dtype=torch.float16, device=gpu)))
     log(f"five-layer step: kernel={kvb.selected_kernel_name(layers[0]['shape'], layers[0]['inp'], SPLIT_TOKENS, True)}")
     stream = torch.cuda.Stream()
+    torch.cuda.synchronize()  # the caches were generated on the default stream
 
     def step():
         for L in layers:
