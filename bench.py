@@ -50,6 +50,7 @@ def main():
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="skip the hipGraph replay (profiling runs)")
     ap.add_argument("--no-five-layer", action="store_true", help="skip the five-layer graph step (configs[4])")
+    ap.add_argument("--no-batched", action="store_true", help="skip the batched configs[2] / configs[3] timings")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run known-size copy and read kernels (for scaling rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -275,6 +276,54 @@ def main():
         log(f"five-layer graph step: {step_us:.2f} us ({five['GB/s']:.0f} GB/s)")
         del extra, lbufs
 
+    # ---- BASELINE configs[2] (16 ragged sequences) and configs[3] (4 x 131072
+    # tokens, GQA 8): one single-launch batched call each, back to back.  Each
+    # cache (about 0.57 GB and 1.1 GB) is larger than the MALL on its own.
+    batched = None
+    if not args.no_batched:
+        batched = {}
+        cfgs = (("cfg3", W.CFG3, W.cfg3_lengths(), 0x4B56423), ("cfg4", W.CFG4, W.CFG4["lengths"], 0x4B56424))
+        for label, cfg, lengths, seed in cfgs:
+            bshape, bt, blens = W.torch_batch(cfg["rows"], cfg["q_heads"], cfg["kv_heads"], cfg["dim"],
+                                              cfg["page_tokens"], lengths, seed=seed,
+                                              split_tokens=cfg["split_tokens"],
+                                              outlier_frac=cfg.get("outlier_frac", 0.0))
+            binp = kvb.batch_input(bt["q"], bt["qpos"], bt["starts"], bt["offsets"], bt["kpos"], bt["table"],
+                                   bt["k"], bt["v"], bt["ks"], bt["vs"])
+            brh = kvb.batch_output_scalar_elements(bshape)
+            bsc = torch.empty(kvb.batch_scratch_elements(bshape), dtype=torch.float32, device=dev)
+            bcnt = torch.zeros(bshape.batch * bshape.kv_heads, dtype=torch.int32, device=dev)
+            bm, bl = torch.empty(brh, dtype=torch.float32, device=dev), torch.empty(brh, dtype=torch.float32,
+                                                                                      device=dev)
+            bn = torch.empty(brh * bshape.dim, dtype=torch.float32, device=dev)
+            bo = torch.empty(brh * bshape.dim, dtype=torch.float16, device=dev)
+
+            def bcall():
+                kvb.decode_attention_batched(bshape, binp, bsc, bm, bl, bn, bo, kvb.KVB_OUT_F16, counters=bcnt,
+                                             stream=sp)
+
+            for _ in range(10):
+                bcall()
+            torch.cuda.synchronize()
+            breps = max(20, args.steps // 10)
+            e0.record(stream)
+            for _ in range(breps):
+                bcall()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            bus = e0.elapsed_time(e1) * 1e3 / breps
+            bbytes = sum(blens) * bshape.kv_heads * (2 * bshape.dim + 8)
+            bgbs = bbytes / (bus * 1e-6) / 1e9
+            batched[label] = {"sequences": bshape.batch, "tokens": sum(blens), "q_heads": bshape.q_heads,
+                              "kv_bytes_per_call": bbytes, "us_per_call": round(bus, 3), "GB/s": round(bgbs, 1),
+                              "pct_of_peak": round(100.0 * bgbs / HBM_PEAK_GBS, 2),
+                              "kernel": kvb.batch_kernel_name(bshape, binp, fused=True),
+                              "splits_per_seq_max": kvb.batch_split_count(bshape)}
+            log(f"{label} batched single-launch call: {bus:.2f} us ({bgbs:.0f} GB/s, "
+                f"{100.0 * bgbs / HBM_PEAK_GBS:.1f}% of peak)")
+            del bt, bsc, bm, bl, bn, bo, bcnt
+            torch.cuda.empty_cache()
+
     # ---- known-size kernels for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE
     if args.calibrate:
         cal_bytes = 256 << 20
@@ -347,6 +396,7 @@ def main():
                          "pct_of_peak": round(100.0 * probe_gbs / HBM_PEAK_GBS, 2),
                          "note": "one plain streaming-read launch of the call's KV byte count, rotated buffers"},
         "five_layer_step": five,
+        "batched": batched,
         "cpu_baseline": cpu,
         "parity": parity,
     }

@@ -201,8 +201,10 @@ struct I8Layout {
   static constexpr uint32_t kExch = NC * 16 * kExchCol;
   static constexpr uint32_t kDig = NC * 16 * kDigCol;
   static constexpr uint32_t kWave = kExch + kDig;
-  static constexpr uint32_t kCombine = NW * 16 * (D + 2) * 4;
-  static constexpr uint32_t kBytes = NW * kWave > kCombine ? NW * kWave : kCombine;
+  // Wave combine area after the exchange areas: [NW][HS] maxima, [NW][HS]
+  // denominators, [NW][HS][D] numerators.
+  static constexpr uint32_t kComb = NW * kWave;
+  static constexpr uint32_t kBytes = kComb + NW * HS * (D + 2) * 4;
 };
 
 // Agent-scope (all XCDs) coherent load of a partial written by another
@@ -771,17 +773,22 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
     });
   }
 
-  // ---- combine the waves through LDS and write the split partial.
-  __syncthreads();
-  float* wm_s = reinterpret_cast<float*>(smem);   // [NW][16]
-  float* wl_s = wm_s + NW * 16;                   // [NW][16]
-  float* wacc_s = wl_s + NW * 16;                 // [NW][16][D]
+  // ---- combine the waves through LDS and write the split partial.  Each
+  // wave publishes its maxima, denominators and numerators in its own rows
+  // of the combine area (disjoint from every exchange area, so no barrier is
+  // needed before), then one barrier.  Each output then requests the NW
+  // wave values of its column together (independent LDS loads, one latency)
+  // and adds them in wave order; a wave with no visible token (m = -inf)
+  // contributes factor 0 to its zero values, which leaves the sum unchanged.
+  float* const wm_s = reinterpret_cast<float*>(smem + L::kComb);  // [NW][HS]
+  float* const wl_s = wm_s + NW * HS;                              // [NW][HS]
+  float* const wacc_s = wl_s + NW * HS;                            // [NW][HS][D]
 #pragma unroll
   for (int h = 0; h < HS; ++h) {
     const float lsum = wave_sum(lrun[h]);
     if (lane == 0) {
-      wm_s[wave * 16 + h] = m_run[h] * kLn2;
-      wl_s[wave * 16 + h] = lsum;
+      wm_s[wave * HS + h] = m_run[h] * kLn2;
+      wl_s[wave * HS + h] = lsum;
     }
   }
   if (n < uint32_t(HS)) {
@@ -792,25 +799,32 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
       y.y = acc_f[mb][1];
       y.z = acc_f[mb][2];
       y.w = acc_f[mb][3];
-      *reinterpret_cast<float4*>(&wacc_s[(wave * 16 + n) * D + 16 * mb + 4 * g]) = y;
+      *reinterpret_cast<float4*>(&wacc_s[(wave * HS + n) * D + 16 * mb + 4 * g]) = y;
     }
   }
   __syncthreads();
   constexpr uint32_t W = D + 2;
   for (uint32_t idx = threadIdx.x; idx < head_rows * W; idx += 64u * NW) {
     const uint32_t hh = idx / W, col = idx % W;
-    float mm = wm_s[hh];
+    // column 1: denominators wl_s[w][hh]; columns 2..: numerators wacc_s[w][hh][col - 2]
+    const float* const xb = col == 1 ? wl_s + hh : wacc_s + hh * D + (col >= 2u ? col - 2u : 0u);
+    const uint32_t xs = col == 1 ? uint32_t(HS) : uint32_t(HS) * D;
+    float mw[NW], xw[NW];
 #pragma unroll
-    for (int w = 1; w < NW; ++w) mm = fmaxf(mm, wm_s[w * 16 + hh]);
+    for (int w = 0; w < NW; ++w) {
+      mw[w] = wm_s[w * HS + hh];
+      xw[w] = xb[w * xs];
+    }
+    float mm = mw[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) mm = fmaxf(mm, mw[w]);
     float val = mm;
     if (col > 0) {
       val = 0.f;
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        const float mw = wm_s[w * 16 + hh];
-        if (mw == neg_inf()) continue;
-        const float f = exp_e(mw - mm);
-        val = fmaf(f, col == 1 ? wl_s[w * 16 + hh] : wacc_s[(w * 16 + hh) * D + col - 2], val);
+        const float f = mw[w] == neg_inf() ? 0.f : exp_e(mw[w] - mm);
+        val = fmaf(f, xw[w], val);
       }
     }
     const uint32_t row2 = hh / a.group, head2 = kv * a.group + hh % a.group;
