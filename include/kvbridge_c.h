@@ -104,9 +104,10 @@ int kvb_decode_attention(const kvb_shape* s, const kvb_device_input* in, uint32_
                          void* stream);
 /* Extension (no counterpart in the reference library; for decode loops that
  * want one launch per call): kvb_decode_attention as a single kernel where
- * the int8-MFMA split kernel serves the shape -- the last work-group to finish
- * for each kv head merges that head's splits (log-sum-exp, split order) into
- * m, l, n and out.  Otherwise it runs the two launches of
+ * the int8-MFMA split kernel serves the shape and its in-kernel merge is
+ * short (at most two 16-byte-load passes over the splits) -- the last
+ * work-group to finish for each kv head merges that head's splits
+ * (log-sum-exp) into m, l, n and out.  Otherwise it runs the two launches of
  * kvb_decode_attention.  `counters` holds kv_heads uint32 that must be zero
  * before the first call; every call leaves them zero (allocate and zero them
  * once, e.g. next to the scratch buffer).  Calls sharing `counters` must not
@@ -158,8 +159,11 @@ int kvb_batch_output_scalar_elements(const kvb_batch_shape* s, size_t* elements)
  * out (KVB_OUT_*), in the batch's row-head order.  counters == NULL: two
  * launches (split, merge).  counters != NULL (batch * kv_heads uint32, zero
  * before the first call and left zero by every call): one launch where the
- * int8-MFMA kernel serves the shape, the last work-group of each
- * (sequence, kv head) merging its splits; otherwise two launches. */
+ * int8-MFMA kernel serves the shape and its in-kernel merge is short (as
+ * for kvb_decode_attention_fused), the last work-group of each
+ * (sequence, kv head) merging its splits; otherwise two launches.  The
+ * single launch writes partials only for each sequence's own splits (the
+ * rest of its scratch rows are left as they were). */
 int kvb_decode_attention_batched(const kvb_batch_shape* s, const kvb_batch_input* in, float* scratch,
                                  uint32_t* counters, float* m, float* l, float* n, void* out, int out_type,
                                  void* stream);

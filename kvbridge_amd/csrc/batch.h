@@ -35,7 +35,9 @@ __device__ __forceinline__ SeqExtent seq_extent(const SplitArgs& a, uint32_t b) 
 // q, q_positions, scratch, counters and the outputs, its k_positions and
 // page-table slice, and the token interval [0, T_b).  Splits past the
 // sequence's own count see an empty interval and write empty partials
-// (m = -inf, l = 0, n = 0), which every merge skips.
+// (m = -inf, l = 0, n = 0), which every merge skips; the single-launch
+// kernel instead ends those work-groups at once and merges only the
+// sequence's own splits.
 __device__ __forceinline__ void rebase_sequence(SplitArgs& a, uint32_t b) {
   const SeqExtent e = seq_extent(a, b);
   const size_t rh0 = size_t(b) * a.rows * a.q_heads;

@@ -502,7 +502,7 @@ int kvb_decode_attention_batched(const kvb_batch_shape* sp, const kvb_batch_inpu
     const auto st = static_cast<hipStream_t>(stream);
     kvb::SplitArgs a = batch_split_args(b, *ip, scratch);
     const bool i8 = batch_uses_i8(b, *ip, a);
-    if (i8 && counters) {
+    if (i8 && counters && kvb::i8_fusable(a)) {
       a.counters = counters;
       a.m = m;
       a.l = l;
@@ -526,7 +526,7 @@ const char* kvb_batch_kernel_name(const kvb_batch_shape* sp, const kvb_batch_inp
   kvb::SplitArgs a = batch_split_args(b, *ip, nullptr);
   const bool i8 = batch_uses_i8(b, *ip, a);
   static uint32_t dummy_counter;  // only its non-nullness is read
-  if (fused && i8) a.counters = &dummy_counter;
+  if (fused && i8 && kvb::i8_fusable(a)) a.counters = &dummy_counter;
   return kvb::split_kernel_name(a, i8, b.int8);
 }
 

@@ -44,6 +44,7 @@
 #include "batch.h"
 #include "device_common.h"
 #include "lds_stream.h"
+#include "merge_rows.h"
 
 namespace kvb {
 namespace {
@@ -218,9 +219,11 @@ __device__ __forceinline__ float ld_agent(const float* p) {
 // M = max_j m_j; L = sum_{l_j > 0} e^{m_j - M} l_j; N[d] likewise (N summed
 // in split order, L by a wave tree); an all-empty head-row gives M = -inf,
 // L = 0, N = 0.  Optional normalized output out = L > 0 ? N / L : 0 (fp32 or
-// fp16).  f_s: LDS [8][32] split factors, ml_s: LDS [8][2] (M, L).
-template <int D, int NW>
-__device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uint32_t head_rows,
+// fp16).  Splits 0 .. ns-1 are merged; a.splits is the partial stride.
+// f_s: LDS [8][32] split factors (the merge_rows area when that runs),
+// ml_s: LDS [8][2] (M, L).
+template <int D, int NW, int HS>
+__device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uint32_t head_rows, uint32_t ns,
                                             const float* __restrict__ scratch, float* f_s, float* ml_s) {
   constexpr uint32_t W = D + 2;
   constexpr uint32_t kCh = 32;  // splits per pass
@@ -233,11 +236,11 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
   // wave): straight-line code that requests every operand at once -- the
   // wave's (m_j, l_j) and the thread's 32 numerators, split indices clamped
   // instead of branched on -- so the merge costs one memory round trip.
-  if (a.splits <= kCh && outs <= 64u * NW && head_rows <= uint32_t(NW)) {
-    const uint32_t jmax = a.splits - 1u;
+  if (ns <= kCh && outs <= 64u * NW && head_rows <= uint32_t(NW)) {
+    const uint32_t jmax = ns - 1u;
     const bool fw = wave < head_rows;
     const float* fb = scratch + row_head(fw ? wave : 0u) * a.splits * W;
-    const uint32_t jl = lane < a.splits ? lane : jmax;
+    const uint32_t jl = lane < ns ? lane : jmax;
     const float mj = ld_agent(fb + size_t(jl) * W);
     const float lj = ld_agent(fb + size_t(jl) * W + 1);
     const bool ot = tid < outs;
@@ -247,7 +250,7 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
 #pragma unroll
     for (uint32_t j = 0; j < kCh; ++j) pre[j] = ld_agent(nb + size_t(j < jmax ? j : jmax) * W);
     if (fw) {
-      const bool in = lane < a.splits;
+      const bool in = lane < ns;
       const float mx = wave_max(in ? mj : neg_inf());
       const float f = in && lj > 0.f ? exp_e(mj - mx) : 0.f;
       const float lsum = wave_sum(f * lj);
@@ -279,9 +282,39 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
     }
     return;
   }
+  // Otherwise, where a thread can own four columns of a head-row: merge_rows
+  // (16-byte agent-coherent loads by split groups, one round trip per pass).
+  if constexpr (uint32_t(HS) * D / 4u <= 64u * NW) {
+    merge_rows<D, NW, HS, true>(
+        head_rows, ns, [&](uint32_t hh) { return scratch + row_head(hh) * a.splits * W; }, f_s,
+        [&](uint32_t hh, uint32_t q, float4 nv, float mv, float lv) {
+          const size_t rh = row_head(hh);
+          if (q == 0) {
+            a.m[rh] = mv;
+            a.l[rh] = lv;
+          }
+          float* const nd = a.n + rh * D + 4u * q;  // caller buffers need only 4-byte alignment
+          nd[0] = nv.x;
+          nd[1] = nv.y;
+          nd[2] = nv.z;
+          nd[3] = nv.w;
+          if (a.out_type != 0) {
+            const float o[4] = {lv > 0.f ? nv.x / lv : 0.f, lv > 0.f ? nv.y / lv : 0.f,
+                                lv > 0.f ? nv.z / lv : 0.f, lv > 0.f ? nv.w / lv : 0.f};
+            if (a.out_type == 1) {
+              float* const od = static_cast<float*>(a.out) + rh * D + 4u * q;
+              for (int i = 0; i < 4; ++i) od[i] = o[i];
+            } else {
+              _Float16* const oh = static_cast<_Float16*>(a.out) + rh * D + 4u * q;
+              for (int i = 0; i < 4; ++i) oh[i] = (_Float16)o[i];
+            }
+          }
+        });
+    return;
+  }
   // General case: passes of 32 splits; the running numerator goes through n.
-  for (uint32_t j0 = 0; j0 < a.splits; j0 += kCh) {
-    const uint32_t cnt = a.splits - j0 < kCh ? a.splits - j0 : kCh;
+  for (uint32_t j0 = 0; j0 < ns; j0 += kCh) {
+    const uint32_t cnt = ns - j0 < kCh ? ns - j0 : kCh;
     for (uint32_t hh = wave; hh < head_rows; hh += NW) {
       const float* base = scratch + row_head(hh) * a.splits * W;
       const bool in = lane < cnt;  // lanes >= 32 idle
@@ -290,7 +323,7 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
       float mx;
       if (j0 == 0) {  // M over every split (later passes reuse it)
         mx = mj;
-        for (uint32_t j = kCh + lane; j < a.splits; j += 64u) mx = fmaxf(mx, ld_agent(base + size_t(j) * W));
+        for (uint32_t j = kCh + lane; j < ns; j += 64u) mx = fmaxf(mx, ld_agent(base + size_t(j) * W));
         mx = wave_max(mx);
       } else {
         mx = ml_s[2 * hh];
@@ -319,7 +352,7 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
 #pragma unroll
         for (uint32_t j = 0; j < kCh; ++j) nacc = fmaf(fh[j], j < cnt ? nv[j] : 0.f, nacc);
       }
-      if (j0 + kCh < a.splits) {
+      if (j0 + kCh < ns) {
         a.n[rh * D + d] = nacc;  // running numerator, re-read by this thread next pass
         continue;
       }
@@ -371,6 +404,15 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
   const uint32_t split = blockIdx.x;
   const uint32_t kv = blockIdx.y;
   const uint32_t head_rows = a.rows * a.group;  // <= HS
+  // Splits that take part in the fused merge.  A batched single-launch call
+  // merges only the sequence's own splits (at least one, so that an empty
+  // sequence still gets its empty result); work-groups past them write no
+  // partial and take no ticket.
+  uint32_t nsplit = a.splits;
+  if constexpr (VARLEN && FUSED) {
+    nsplit = a.end > 0u ? (a.end - 1u) / a.split_tokens + 1u : 1u;
+    if (split >= nsplit) return;
+  }
 
   const uint64_t s0_64 = uint64_t(a.begin) + uint64_t(split) * a.split_tokens;
   const uint32_t s0 = s0_64 < a.end ? uint32_t(s0_64) : a.end;
@@ -848,12 +890,14 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
     __syncthreads();
     if (threadIdx.x == 0) {
       const uint32_t t = __hip_atomic_fetch_add(a.counters + kv, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last_s = t + 1u == a.splits ? 1u : 0u;
+      last_s = t + 1u == nsplit ? 1u : 0u;
     }
     __syncthreads();
     if (last_s != 0u) {
-      float* f_s = reinterpret_cast<float*>(smem);  // [HS][32] split factors
-      fused_merge<D, NW>(a, kv, head_rows, scratch, f_s, f_s + HS * 32);
+      static_assert(MergeRowsLayout<D, NW, (uint32_t(HS) * D / 4u <= 64u * NW ? HS : 1)>::kFloats * 4u <= L::kBytes,
+                    "the merge's LDS fits the kernel's");
+      float* f_s = reinterpret_cast<float*>(smem);  // [HS][32] split factors or the merge_rows area
+      fused_merge<D, NW, HS>(a, kv, head_rows, nsplit, scratch, f_s, f_s + HS * 32);
       if (threadIdx.x == 0) __hip_atomic_store(a.counters + kv, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }

@@ -19,9 +19,16 @@ namespace {
 
 constexpr uint32_t kTiles = 64;  // tokens per tile
 
-// (waves, ring slots) per work-group as 10 * NW + NB, by tiles per split:
-// eight waves (two per SIMD, <= 256 registers each) where the state fits
-// (head_rows <= 4, dim <= 128) and the split has >= 16 tiles.
+// (waves, ring slots) per work-group as 10 * NW + NB.  A grid of at most
+// two work-groups per CU of a 256-CU device: eight waves (two per SIMD,
+// <= 256 registers each) where the state fits (head_rows <= 4, dim <= 128)
+// and the split has >= 16 tiles.  Larger grids (batches) run several rounds
+// of work-groups per CU, and smaller work-groups that share a CU hide each
+// other's prologue and combine: four waves (two per SIMD) for <= 4
+// head-rows, two waves for 8 head-rows (whose state takes one SIMD per
+// wave).  Measured on MI355X (configs[2] / configs[3] batched calls,
+// 2048-work-group grids): 118 / 216 us with these against 140 / 242 us with
+// the single-sequence choice.
 // KVB_I8_CFG="NW,NB" overrides (tuning sweeps; unknown pairs fall back).
 int i8_config(const SplitArgs& a) {
   static const int forced = [] {
@@ -30,8 +37,11 @@ int i8_config(const SplitArgs& a) {
     return std::atoi(e) * 10 + std::atoi(e + 2);
   }();
   const uint32_t tiles = (a.split_tokens + kTiles - 1) / kTiles;
-  const bool eight = a.rows * a.group <= 4 && a.dim <= 128;
+  const uint32_t hr = a.rows * a.group;
+  const bool eight = hr <= 4 && a.dim <= 128;
   if (forced == 42 || forced == 22 || ((forced == 82 || forced == 44) && eight)) return forced;
+  const uint64_t groups = uint64_t(a.splits) * a.kv_heads * (a.seq_starts ? a.batch : 1u);
+  if (groups > 512u) return hr <= 4 && tiles >= 4 ? 42 : 22;
   if (eight && tiles >= 16) return 82;
   return tiles >= 4 ? 42 : 22;
 }
@@ -50,7 +60,21 @@ bool i8_supported(const SplitArgs& a) {
   return true;
 }
 
-bool i8_fusable(const SplitArgs& a) { return i8_supported(a); }
+// The in-kernel merge of the single launch is worth it where it is short:
+// the straight-line path (<= 32 splits, a thread per output, a wave per
+// head-row) or at most two merge_rows passes with a thread per four columns;
+// larger merges (e.g. 8 head-rows on two-wave work-groups) run faster as the
+// stand-alone merge kernel, whose work-groups spread over every CU.
+bool i8_fusable(const SplitArgs& a) {
+  if (!i8_supported(a)) return false;
+  const uint32_t nw = uint32_t(i8_config(a)) / 10u, threads = 64u * nw;
+  const uint32_t hr = a.rows * a.group, hs = hr <= 4 ? 4u : 8u;
+  if (a.splits <= 32 && hr * a.dim <= threads && hr <= nw) return true;
+  const uint32_t quads = hs * a.dim / 4u;
+  if (quads > threads) return false;
+  const uint32_t groups = threads / quads, per_pass = groups * (groups >= 8 ? 64u / groups : 8u);
+  return (a.splits + per_pass - 1u) / per_pass <= 2u;
+}
 
 hipError_t launch_split_i8(const SplitArgs& a, hipStream_t stream) {
   const int cfg = i8_config(a);

@@ -44,6 +44,8 @@ FUSED_SHAPES = [
     (1, 8, 2, 64, 16, 4096, 0, 4096, 64, None),         # 64 splits: merge in two chunks
     (1, 32, 8, 128, 64, 8192, 5, 8192, 64, [6000]),     # 128 splits, causal cut, ragged begin
     (2, 8, 2, 128, 32, 2000, 0, 2000, 32, [1999, 700]), # 8 head-rows, 63 splits
+    (1, 32, 8, 128, 64, 4096, 0, 4096, 256, None),      # four-wave groups: one 16-split merge pass
+    (1, 64, 8, 128, 64, 4096, 0, 4096, 256, [3000]),    # 8 head-rows, 16 splits: two 8-split passes
 ]
 
 
@@ -53,8 +55,9 @@ def test_fused_matches_oracle_and_two_launch(gpu, cfg):
 
     rows, qh, kvh, d, p, t, b, e, st, qpos = cfg
     case = W.synth_case(rows, qh, kvh, d, p, t, seed=zlib.crc32(repr(cfg).encode()) & 0xFFFF, begin=b, end=e, qpos=qpos)
-    log(f"fused shape={case.shape.as_tuple()} split_tokens={st} kernel={kvb.selected_kernel_name(case.shape, DeviceCase(case).inp, st)}")
     dc = DeviceCase(case)
+    log(f"fused shape={case.shape.as_tuple()} split_tokens={st} "
+        f"kernel={kvb.selected_kernel_name(case.shape, dc.inp, st, True)}")
     counters = torch.zeros(kvh, dtype=torch.int32, device=gpu)
     ref = O.fp64(case, threads=8)
     mln, out = run_fused(dc, st, counters)
