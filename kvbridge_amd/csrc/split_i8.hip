@@ -64,9 +64,13 @@ bool i8_supported(const SplitArgs& a) {
 // the straight-line path (<= 32 splits, a thread per output, a wave per
 // head-row) or at most two merge_rows passes with a thread per four columns;
 // larger merges (e.g. 8 head-rows on two-wave work-groups) run faster as the
-// stand-alone merge kernel, whose work-groups spread over every CU.
+// stand-alone merge kernel, whose work-groups spread over every CU.  Grids
+// of more than two work-groups per CU (batches) also run two launches: every
+// work-group's ticket and the merges then sit between rounds of split work
+// (configs[2]: 116 us for two launches against 121-123 us for one).
 bool i8_fusable(const SplitArgs& a) {
   if (!i8_supported(a)) return false;
+  if (uint64_t(a.splits) * a.kv_heads * (a.seq_starts ? a.batch : 1u) > 512u) return false;
   const uint32_t nw = uint32_t(i8_config(a)) / 10u, threads = 64u * nw;
   const uint32_t hr = a.rows * a.group, hs = hr <= 4 ? 4u : 8u;
   if (a.splits <= 32 && hr * a.dim <= threads && hr <= nw) return true;

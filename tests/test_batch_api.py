@@ -79,13 +79,15 @@ def test_kernel_choice_names():
     assert kvb.batch_kernel_name(s, inp) == "split_i8_kernel<128,2,2,true,8,false,true>"
     # one sequence: 512 work-groups -> four-wave groups
     assert kvb.batch_kernel_name(s.copy(batch=1), inp) == "split_i8_kernel<128,4,2,true,8,false,true>"
-    # 4 head-rows, 2048 work-groups -> four waves (one merge pass of 16 splits: single launch);
-    # 256 work-groups -> eight waves
+    # 4 head-rows, 2048 work-groups -> four waves, two launches (more than two work-groups per CU);
+    # 512 work-groups -> eight-wave single launch; 256 -> eight waves
     g4 = s.copy(q_heads=32)
     assert kvb.batch_kernel_name(g4, inp) == "split_i8_kernel<128,4,2,true,4,false,true>"
-    assert kvb.batch_kernel_name(g4.copy(batch=16, max_tokens=32768), inp, fused=True) == \
-        "split_i8_kernel<128,4,2,true,4,true,true>"
     assert kvb.batch_kernel_name(g4, inp, fused=True) == "split_i8_kernel<128,4,2,true,4,false,true>"
+    assert kvb.batch_kernel_name(g4.copy(batch=16, max_tokens=32768), inp, fused=True) == \
+        "split_i8_kernel<128,4,2,true,4,false,true>"
+    assert kvb.batch_kernel_name(g4.copy(max_tokens=32768), inp, fused=True) == \
+        "split_i8_kernel<128,8,2,true,4,true,true>"
     assert kvb.batch_kernel_name(g4.copy(batch=1, max_tokens=65536), inp) == "split_i8_kernel<128,8,2,true,4,false,true>"
     small_pages = s.copy(page_tokens=16, pages=8192 * 4, table_entries=8192 * 4)
     assert kvb.batch_kernel_name(small_pages, inp).startswith("split_generic_kernel<true, true>")
