@@ -205,7 +205,13 @@ struct I8Layout {
   // Wave combine area after the exchange areas: [NW][HS] maxima, [NW][HS]
   // denominators, [NW][HS][D] numerators.
   static constexpr uint32_t kComb = NW * kWave;
-  static constexpr uint32_t kBytes = kComb + NW * HS * (D + 2) * 4;
+  // Q digit area after it: [64 lanes][kQdBytes] (written before the main
+  // loop, read by every wave; waves with no tiles reach the combine early,
+  // so it must not overlap the combine area).
+  static constexpr bool kPair = D == 128 && HS <= 4;  // paired-row QK layout
+  static constexpr uint32_t kQdBytes = (kPair ? 2 : NC) * (kPair ? 1 : D / 64) * 16;
+  static constexpr uint32_t kQd = kComb + NW * HS * (D + 2) * 4;
+  static constexpr uint32_t kBytes = kQd + 64 * kQdBytes;
 };
 
 // Agent-scope (all XCDs) coherent load of a partial written by another
@@ -393,7 +399,7 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
   // digits holds half h, so rows and tiles of equal half give the two half
   // dot products of a token, which add exactly in int32.  The K loads of a
   // k-block then read whole 64-byte half rows, two per 128-byte line.
-  constexpr bool PAIR = D == 128 && HS <= 4;
+  constexpr bool PAIR = L::kPair;
   constexpr int NCQ = PAIR ? 2 : NC;        // MFMA column tiles of the QK B operand
   constexpr int KS = PAIR ? 1 : D / 64;     // 64-dim steps per QK M-block
   __shared__ __attribute__((aligned(16))) uint8_t smem[L::kBytes];
@@ -542,9 +548,15 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
 
   // ---- Q digits (B operand of QK) and per-head score factors.  A column's
   // scale 2^kq comes from its head-row's whole Q row (with PAIR both tiles
-  // of a lane hold the same column).
+  // of a lane hold the same column).  Every wave needs the same digits (its
+  // lanes are the same MFMA columns), so the digit dwords are built once per
+  // work-group: wave w builds dwords d = w, w + NW, ... of every lane and
+  // stores them in the Q digit area of LDS; after one barrier (LDS only: the
+  // first KV item stays in flight) each wave reads its lanes' digits back.
   i32x4 qd[NCQ][KS];
   float cql[HS];
+  static_assert(L::kQdBytes == NCQ * KS * 16, "digit bytes per lane");
+  uint8_t* const qd_s = smem + L::kQd + lane * L::kQdBytes;
   {
     int kq_lane = 0;
     auto col_kq = [&](float amax) __attribute__((always_inline)) {
@@ -580,9 +592,10 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
       if (nc == 0) kq_lane = kq;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        uint32_t w[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
+          const uint32_t dw = (uint32_t(nc) * KS + s) * 4u + j;  // digit dword of the lane
+          if (dw % NW != wave) continue;                       // uniform: built by wave dw % NW
           uint32_t packed = 0;
 #pragma unroll
           for (int b = 0; b < 4; ++b) {
@@ -594,11 +607,18 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
             const int d = dg == 0 ? hi : (dg == 1 ? mid : lo);
             packed |= (uint32_t(d) & 0xffu) << (8 * b);
           }
-          w[j] = valid ? packed : 0u;
+          *reinterpret_cast<uint32_t*>(qd_s + 4u * dw) = valid ? packed : 0u;
         }
-        qd[nc][s] = i32x4{int(w[0]), int(w[1]), int(w[2]), int(w[3])};
       }
     }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int nc = 0; nc < NCQ; ++nc)
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const u32x4_t w = *reinterpret_cast<const u32x4_t*>(qd_s + 16u * (uint32_t(nc) * KS + s));
+        qd[nc][s] = i32x4{int(w[0]), int(w[1]), int(w[2]), int(w[3])};
+      }
 #pragma unroll
     for (int h = 0; h < HS; ++h) {
       const int kq = __builtin_amdgcn_readlane(kq_lane, h);
