@@ -865,36 +865,44 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
     }
   }
   __syncthreads();
+  // One numerator column per thread and iteration (no branches: the LDS
+  // loads of all waves are requested together); the thread of column 0 also
+  // writes the head-row's maximum and denominator.
   constexpr uint32_t W = D + 2;
-  for (uint32_t idx = threadIdx.x; idx < head_rows * W; idx += 64u * NW) {
-    const uint32_t hh = idx / W, col = idx % W;
-    // column 1: denominators wl_s[w][hh]; columns 2..: numerators wacc_s[w][hh][col - 2]
-    const float* const xb = col == 1 ? wl_s + hh : wacc_s + hh * D + (col >= 2u ? col - 2u : 0u);
-    const uint32_t xs = col == 1 ? uint32_t(HS) : uint32_t(HS) * D;
-    float mw[NW], xw[NW];
+  for (uint32_t o = threadIdx.x; o < head_rows * uint32_t(D); o += 64u * NW) {
+    const uint32_t hh = o / D, d = o % D;
+    float mw[NW], lv[NW], xw[NW];
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       mw[w] = wm_s[w * HS + hh];
-      xw[w] = xb[w * xs];
+      lv[w] = wl_s[w * HS + hh];
+      xw[w] = wacc_s[(w * HS + hh) * D + d];
     }
     float mm = mw[0];
 #pragma unroll
     for (int w = 1; w < NW; ++w) mm = fmaxf(mm, mw[w]);
-    float val = mm;
-    if (col > 0) {
-      val = 0.f;
+    float val = 0.f, lsum = 0.f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        const float f = mw[w] == neg_inf() ? 0.f : exp_e(mw[w] - mm);
-        val = fmaf(f, xw[w], val);
-      }
+    for (int w = 0; w < NW; ++w) {
+      const float f = mw[w] == neg_inf() ? 0.f : exp_e(mw[w] - mm);
+      val = fmaf(f, xw[w], val);
+      lsum = fmaf(f, lv[w], lsum);
     }
     const uint32_t row2 = hh / a.group, head2 = kv * a.group + hh % a.group;
-    float* dst = scratch + ((size_t(row2) * a.q_heads + head2) * a.splits + split) * W + col;
-    if constexpr (FUSED)
-      __hip_atomic_store(dst, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // agent-coherent
-    else
-      *dst = val;
+    float* const dst = scratch + ((size_t(row2) * a.q_heads + head2) * a.splits + split) * W;
+    if constexpr (FUSED) {  // agent-coherent
+      __hip_atomic_store(dst + 2 + d, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (d == 0) {
+        __hip_atomic_store(dst, mm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(dst + 1, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    } else {
+      dst[2 + d] = val;
+      if (d == 0) {
+        dst[0] = mm;
+        dst[1] = lsum;
+      }
+    }
   }
 
   // ---- fused merge: the last work-group to finish for this kv head merges
