@@ -413,11 +413,23 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
   // Splits that take part in the fused merge.  A batched single-launch call
   // merges only the sequence's own splits (at least one, so that an empty
   // sequence still gets its empty result); work-groups past them write no
-  // partial and take no ticket.
+  // partial and take no ticket.  In a two-launch batched call they write the
+  // empty partial (m = -inf, l = 0, n = 0) straight away, without loading
+  // anything.
   uint32_t nsplit = a.splits;
-  if constexpr (VARLEN && FUSED) {
+  if constexpr (VARLEN) {
     nsplit = a.end > 0u ? (a.end - 1u) / a.split_tokens + 1u : 1u;
-    if (split >= nsplit) return;
+    if (split >= nsplit) {
+      if constexpr (!FUSED) {
+        constexpr uint32_t W = D + 2;
+        for (uint32_t o = threadIdx.x; o < head_rows * W; o += 64u * NW) {
+          const uint32_t hh = o / W, col = o % W;
+          const uint32_t row2 = hh / a.group, head2 = kv * a.group + hh % a.group;
+          scratch[((size_t(row2) * a.q_heads + head2) * a.splits + split) * W + col] = col == 0 ? neg_inf() : 0.f;
+        }
+      }
+      return;
+    }
   }
 
   const uint64_t s0_64 = uint64_t(a.begin) + uint64_t(split) * a.split_tokens;
