@@ -51,6 +51,9 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="skip the hipGraph replay (profiling runs)")
     ap.add_argument("--no-five-layer", action="store_true", help="skip the five-layer graph step (configs[4])")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched configs[2] / configs[3] timings")
+    ap.add_argument("--no-mma-geometry", action="store_true",
+                    help="skip the rows-8 / group-6 / dim-256 / page-32 launch_attention_mma timing")
+    ap.add_argument("--no-append", action="store_true", help="skip the paged INT8 append timings")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run known-size copy and read kernels (for scaling rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -327,6 +330,85 @@ def main():
             del bt, bsc, bm, bl, bn, bo, bcnt
             torch.cuda.empty_cache()
 
+    # ---- the reference's dense MMA geometry (attention_mma_supported: 8 query
+    # rows sharing the KV, 24 q / 4 kv heads = group 6, dim 256, page 32) at
+    # 65536 tokens: launch_attention_mma (its 256-token splits + merge), back
+    # to back over rotated caches.  KV bytes per call 136,314,880, the byte
+    # count of the reference's own 64K benchmark (data/att-bench-65536-v2-07.json).
+    mma = None
+    if not args.no_mma_geometry:
+        mcaches = [W.torch_cache(8, 24, 4, 256, 32, 65536, seed=0x4B56440 + c, device="cuda:0")
+                   for c in range(args.copies)]
+        ms_ = mcaches[0][0]
+        assert kvb.attention_mma_supported(ms_)
+        minps = [kvb.device_input(t_["q"], t_["qpos"], t_["kpos"], t_["table"], t_["k"], t_["v"], t_["ks"], t_["vs"])
+                 for _, t_ in mcaches]
+        mrh = ms_.rows * ms_.q_heads
+        msc = torch.empty(kvb.scratch_elements(ms_), dtype=torch.float32, device=dev)
+        mm_, ml_ = torch.empty(mrh, device=dev), torch.empty(mrh, device=dev)
+        mn_ = torch.empty(mrh * ms_.dim, device=dev)
+
+        def mcall(i):
+            kvb.launch_attention_mma(ms_, minps[i % len(minps)], msc, mm_, ml_, mn_, sp)
+
+        for i in range(10):
+            mcall(i)
+        torch.cuda.synchronize()
+        mreps = max(50, args.steps // 4)
+        e0.record(stream)
+        for i in range(mreps):
+            mcall(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        mus = e0.elapsed_time(e1) * 1e3 / mreps
+        mbytes = 65536 * ms_.kv_heads * (2 * ms_.dim + 8)
+        mgbs = mbytes / (mus * 1e-6) / 1e9
+        mma = {"shape": "8 rows x 24 q / 4 kv heads, dim 256, page 32, 65536 tokens, 256 splits + merge",
+               "kv_bytes_per_call": mbytes, "us_per_call": round(mus, 3), "GB/s": round(mgbs, 1),
+               "pct_of_peak": round(100.0 * mgbs / HBM_PEAK_GBS, 2),
+               "kernel": kvb.selected_kernel_name(ms_, minps[0], 256)}
+        log(f"mma geometry (launch_attention_mma): {mus:.2f} us ({mgbs:.0f} GB/s, "
+            f"{100.0 * mgbs / HBM_PEAK_GBS:.1f}% of peak)")
+        del mcaches, minps, msc
+        torch.cuda.empty_cache()
+
+    # ---- paged INT8 append (kvb_append_kv): a 4096-token prefill chunk and a
+    # one-token decode step into a cfg2-sized pool, fp16 sources.  Bytes moved
+    # per token and kv head: 2 x dim fp16 read, 2 x dim int8 + 8 B scales written.
+    append = None
+    if not args.no_append:
+        append = {}
+        apages = 1024
+        ak = torch.empty((apages, kvh, P, D), dtype=torch.int8, device=dev)
+        av = torch.empty((apages, kvh, D, P), dtype=torch.int8, device=dev)
+        aks = torch.empty((apages, kvh, P), dtype=torch.float32, device=dev)
+        avs = torch.empty((apages, kvh, P), dtype=torch.float32, device=dev)
+        for ntok in (4096, 1):
+            kn = torch.randn((ntok, kvh, D), device=dev).half()
+            vn = torch.randn((ntok, kvh, D), device=dev).half()
+            slots = torch.randperm(apages * P, device=dev)[:ntok].to(torch.int32)
+            ash = kvb.append_shape(ntok, kvh, D, P, apages, kvb.KVB_SRC_F16)
+
+            def acall():
+                kvb.append_kv(ash, kn, vn, slots, ak, av, aks, avs, stream=sp)
+
+            for _ in range(10):
+                acall()
+            torch.cuda.synchronize()
+            areps = max(100, args.steps // 4)
+            e0.record(stream)
+            for _ in range(areps):
+                acall()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            aus = e0.elapsed_time(e1) * 1e3 / areps
+            abytes = ntok * kvh * (2 * D * 2 + 2 * D + 8)
+            agbs = abytes / (aus * 1e-6) / 1e9
+            append[f"{ntok}_tokens"] = {"bytes_per_call": abytes, "us_per_call": round(aus, 3),
+                                        "GB/s": round(agbs, 1), "pct_of_peak": round(100.0 * agbs / HBM_PEAK_GBS, 2)}
+            log(f"append {ntok} tokens x {kvh} kv heads (fp16 source): {aus:.2f} us ({agbs:.0f} GB/s)")
+        del ak, av, aks, avs
+
     # ---- known-size kernels for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE
     if args.calibrate:
         cal_bytes = 256 << 20
@@ -400,6 +482,8 @@ def main():
                          "note": "one plain streaming-read launch of the call's KV byte count, rotated buffers"},
         "five_layer_step": five,
         "batched": batched,
+        "mma_geometry": mma,
+        "append": append,
         "cpu_baseline": cpu,
         "parity": parity,
     }
