@@ -372,9 +372,11 @@ def main():
         del mcaches, minps, msc
         torch.cuda.empty_cache()
 
-    # ---- paged INT8 append (kvb_append_kv): a 4096-token prefill chunk and a
-    # one-token decode step into a cfg2-sized pool, fp16 sources.  Bytes moved
-    # per token and kv head: 2 x dim fp16 read, 2 x dim int8 + 8 B scales written.
+    # ---- paged INT8 append (kvb_append_kv): a 4096-token prefill chunk (tokens
+    # fill the slots of randomly chosen pages in order, as a paged prefill does)
+    # and a one-token decode step into a cfg2-sized pool, fp16 sources.  Bytes
+    # moved per token and kv head: 2 x dim fp16 read, 2 x dim int8 + 8 B scales
+    # written.
     append = None
     if not args.no_append:
         append = {}
@@ -386,7 +388,8 @@ def main():
         for ntok in (4096, 1):
             kn = torch.randn((ntok, kvh, D), device=dev).half()
             vn = torch.randn((ntok, kvh, D), device=dev).half()
-            slots = torch.randperm(apages * P, device=dev)[:ntok].to(torch.int32)
+            tok = torch.arange(ntok, device=dev)
+            slots = (torch.randperm(apages, device=dev)[tok // P] * P + tok % P).to(torch.int32)
             ash = kvb.append_shape(ntok, kvh, D, P, apages, kvb.KVB_SRC_F16)
 
             def acall():

@@ -34,6 +34,12 @@ CASES = [
     (40, 1, 256, 64, kvb.KVB_SRC_F16, 0),
     (64, 8, 128, 64, kvb.KVB_SRC_BF16, 4096),   # rows inside a wider (fused QKV-like) buffer
     (1, 8, 128, 64, kvb.KVB_SRC_F32, 0),        # one decode-step token
+    # >= 256 tokens: the tile kernel (lane = token)
+    (300, 8, 128, 64, kvb.KVB_SRC_F16, 0),       # 16-byte loads and K stores
+    (400, 3, 67, 32, kvb.KVB_SRC_F32, 0),        # odd dim: element path
+    (260, 1, 256, 64, kvb.KVB_SRC_BF16, 0),
+    (512, 8, 128, 64, kvb.KVB_SRC_BF16, 4096),   # rows inside a wider buffer
+    (257, 2, 100, 16, kvb.KVB_SRC_F16, 3),       # stride not a 16-byte multiple: element path
 ]
 
 
