@@ -191,9 +191,17 @@ __global__ __launch_bounds__(64 * NW) void split_lds_kernel(
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t h = lane & 15u, g = lane >> 4;
-  const uint32_t split = blockIdx.x;
-  const uint32_t kv = blockIdx.y % a.kv_heads, hblock = blockIdx.y / a.kv_heads;
   const uint32_t head_rows = a.rows * a.group;
+  // Work-group -> (split, kv head, block of 16 head-rows).  The blocks of one
+  // (split, kv head) read the same KV tiles, so they get consecutive ids
+  // congruent mod 8: dispatched together, and on the same XCD where
+  // work-groups are dealt to the 8 XCDs round-robin, where the later blocks'
+  // reads then hit that XCD's L2 (a locality choice only).
+  const uint32_t hblocks = (head_rows + 15u) / 16u;
+  const uint32_t id = blockIdx.x, xr = id % 8u, xt = id / 8u;
+  const uint32_t hblock = xt % hblocks, unit = 8u * (xt / hblocks) + xr;
+  if (unit >= a.splits * a.kv_heads) return;  // grid padding
+  const uint32_t split = unit % a.splits, kv = unit / a.splits;
   const uint32_t hr = hblock * 16u + h;
   const bool hvalid = hr < head_rows;
   const uint32_t row = hvalid ? hr / a.group : 0u;
@@ -414,14 +422,202 @@ __global__ __launch_bounds__(64 * NW) void split_lds_kernel(
   }
 }
 
+// Many head-row blocks over short splits (e.g. the reference's dense
+// rows-8 / group-6 geometry, 48 head-rows = 3 blocks, 256-token splits): one
+// work-group per (split, kv head) DMAs the split's whole tiles into LDS once
+// (tile j by wave j % 4), and after one barrier wave w runs head-row blocks
+// w, w + 4, ... over every tile with the online softmax of compute_tile.  A
+// wave owns whole head-rows, so it writes their partials straight from its
+// registers: no wave combine, and the KV bytes of a (split, kv head) are
+// read once instead of once per block.  Requires splits that start on a
+// tile boundary and hold at most TM tiles (host-checked).
+constexpr int kRowsWaves = 4;
+
+template <int D, int TM, bool PT>
+__global__ __launch_bounds__(64 * kRowsWaves) void split_lds_rows_kernel(
+    SplitArgs a, const float* __restrict__ q, const int64_t* __restrict__ qpos,
+    const int64_t* __restrict__ kpos, const uint32_t* __restrict__ table,
+    const int8_t* __restrict__ kdata, const int8_t* __restrict__ vdata,
+    const float* __restrict__ kscale, const float* __restrict__ vscale, float* __restrict__ scratch) {
+  using G = Geo<D>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[TM * G::kBufBytes];
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t h = lane & 15u, g = lane >> 4;
+  const uint32_t split = blockIdx.x, kv = blockIdx.y;
+  const uint32_t head_rows = a.rows * a.group, hblocks = (head_rows + 15u) / 16u;
+
+  const uint64_t s0_64 = uint64_t(a.begin) + uint64_t(split) * a.split_tokens;
+  const uint32_t s0 = s0_64 < a.end ? uint32_t(s0_64) : a.end;
+  const uint32_t s1 = uint64_t(s0) + a.split_tokens < a.end ? s0 + a.split_tokens : a.end;
+  const uint32_t k_first = s0 / kTileTokens;
+  const uint32_t ntiles = s1 > s0 ? (s1 - 1u) / kTileTokens + 1u - k_first : 0u;  // <= TM
+
+  // ---- every tile of the split into LDS (tile j -> buffer j, by wave j % 4)
+  if (ntiles > 0) {
+    Ctx c;
+    c.k = kdata;
+    c.v = vdata;
+    c.ks = kscale;
+    c.vs = vscale;
+    c.table = table;
+    c.kv = kv;
+    c.kv_heads = a.kv_heads;
+    c.P = a.page_tokens;
+    c.pages = a.pages;
+    c.lp_lo = s0 / a.page_tokens;
+    c.lp_hi = (s1 - 1u) / a.page_tokens;
+    c.lane = lane;
+    {
+      const uint32_t lp = c.lp_lo + lane;
+      c.ptab = lp <= c.lp_hi ? table[lp] : 0u;
+    }
+    PtCtx pc;
+    if constexpr (PT) {
+      const uint32_t kv_bytes = a.pages * a.kv_heads * a.page_tokens * uint32_t(D);
+      const uint32_t sc_bytes = a.pages * a.kv_heads * a.page_tokens * 4u;
+      pt_init<D>(pc, kdata, vdata, kscale, vscale, kv_bytes, sc_bytes, a.page_tokens, lane);
+    }
+    for (uint32_t j = wave; j < ntiles; j += kRowsWaves) {
+      uint8_t* const buf = smem + j * G::kBufBytes;
+      const uint32_t k = k_first + j;
+      if constexpr (PT) {
+        const uint32_t lp = k * kTileTokens / a.page_tokens;
+        const uint32_t rel = lp - c.lp_lo;
+        uint32_t phys = rel < 64u ? __builtin_amdgcn_readlane(c.ptab, rel) : table[lp];
+        phys = phys < a.pages ? phys : a.pages - 1u;
+        pt_issue<D>(pc, phys * a.kv_heads + kv, k * kTileTokens - lp * a.page_tokens, a.page_tokens, buf);
+      } else {
+        issue_tile<D>(c, k, buf);
+      }
+    }
+  }
+  wait_vm<0>();
+  __syncthreads();
+
+  const ReadOffsets<D> ro = read_offsets<D>(lane);
+  const uint32_t base0 = lds_addr(smem);
+  constexpr uint32_t W = D + 2;
+  for (uint32_t hblock = wave; hblock < hblocks; hblock += kRowsWaves) {
+    const uint32_t hr = hblock * 16u + h;
+    const bool hvalid = hr < head_rows;
+    const uint32_t row = hvalid ? hr / a.group : 0u;
+    const uint32_t head = kv * a.group + (hvalid ? hr % a.group : 0u);
+
+    // ---- visibility: tokens [s0, e_h) are visible to this lane's row.
+    const uint32_t r_lo = hblock * 16u / a.group;
+    const uint32_t r_hi = (hblock * 16u + 15u < head_rows ? hblock * 16u + 15u : head_rows - 1u) / a.group;
+    uint32_t e_h = s0;
+    if (s1 > s0) {
+      const int64_t klast = kpos[s1 - 1u];
+      bool all_visible = true;
+      for (uint32_t r = r_lo; r <= r_hi; ++r) all_visible &= klast <= qpos[r];
+      if (all_visible) {
+        e_h = s1;
+      } else {
+        for (uint32_t r = r_lo; r <= r_hi; ++r) {
+          const uint32_t e = visible_end(kpos, s0, s1, qpos[r], lane);
+          if (row == r) e_h = e;
+        }
+      }
+      if (!hvalid) e_h = s0;
+    }
+    uint32_t e_min = hvalid ? e_h : 0xffffffffu, e_max = e_h;
+#define KVB_ROW_RED(N)                                                                                    \
+  {                                                                                                       \
+    const uint32_t o1 = uint32_t(__builtin_amdgcn_update_dpp(0, int(e_min), 0x120 + N, 0xF, 0xF, false)); \
+    const uint32_t o2 = uint32_t(__builtin_amdgcn_update_dpp(0, int(e_max), 0x120 + N, 0xF, 0xF, false)); \
+    e_min = o1 < e_min ? o1 : e_min;                                                                      \
+    e_max = o2 > e_max ? o2 : e_max;                                                                      \
+  }
+    KVB_ROW_RED(8) KVB_ROW_RED(4) KVB_ROW_RED(2) KVB_ROW_RED(1)
+#undef KVB_ROW_RED
+    e_min = __builtin_amdgcn_readfirstlane(e_min);
+    e_max = __builtin_amdgcn_readfirstlane(e_max);
+
+    // ---- Q as 2^kq-scaled f16 hi + lo (B operand of QK).
+    float qv[D / 4];
+    if (hvalid) {
+      const float4* qp = reinterpret_cast<const float4*>(q + (size_t(row) * a.q_heads + head) * D + g * (D / 4));
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) {
+        const float4 x = qp[i];
+        qv[4 * i] = x.x;
+        qv[4 * i + 1] = x.y;
+        qv[4 * i + 2] = x.z;
+        qv[4 * i + 3] = x.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < D / 4; ++i) qv[i] = 0.f;
+    }
+    float qmax = 0.f;
+#pragma unroll
+    for (int i = 0; i < D / 4; ++i) qmax = fmaxf(qmax, fabsf(qv[i]));
+    qmax = rows_max(qmax);
+    int kq = 0;
+    if (qmax > 0.f) {
+      kq = 15 - __builtin_amdgcn_frexp_expf(qmax);
+      kq = kq < -100 ? -100 : (kq > 100 ? 100 : kq);
+    }
+    const float cq = __builtin_amdgcn_ldexpf(a.scale, -kq);
+    f16x8 qh[D / 32], ql[D / 32];
+    bool any_lo = false;
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = __builtin_amdgcn_ldexpf(qv[8 * s + e], kq);
+        const _Float16 hi = (_Float16)x;
+        const _Float16 lo = (_Float16)(x - (float)hi);
+        qh[s][e] = hi;
+        ql[s][e] = lo;
+        any_lo |= (lo != (_Float16)0.0f);
+      }
+    const bool qlo = __ballot(any_lo) != 0;
+
+    WaveState<D> st;
+#pragma unroll
+    for (int mb = 0; mb < D / 16; ++mb) st.acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.m = neg_inf();
+    st.l = 0.f;
+    st.kexp = 100;
+    const uint32_t k_vis = e_max > s0 ? (e_max - 1u) / kTileTokens : 0u;
+    const uint32_t nvis = e_max > s0 ? k_vis + 1u - k_first : 0u;
+    for (uint32_t j = 0; j < nvis; ++j) {
+      const uint32_t k = k_first + j;
+      const bool full = k * kTileTokens >= s0 && (k + 1u) * kTileTokens <= e_min;
+      compute_tile<D, 0>(st, base0 + j * G::kBufBytes, ro, k, qh, ql, qlo, cq, full, s0, e_h, e_max, lane);
+    }
+
+    // ---- this block's partials, straight from the registers
+    const float l_h = rows_sum(st.l);
+    if (hvalid) {
+      float* const dst = scratch + ((size_t(row) * a.q_heads + head) * a.splits + split) * W;
+      if (g == 0) {
+        dst[0] = st.m;
+        dst[1] = l_h;
+      }
+#pragma unroll
+      for (int mb = 0; mb < D / 16; ++mb) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[2 + 16 * mb + 4 * g + e] = __builtin_amdgcn_ldexpf(st.acc[mb][e], -st.kexp);
+      }
+    }
+  }
+}
+
 #define KVB_LDS_ARGS                                                                             \
   a, a.q, a.q_positions, a.k_positions, a.page_table, static_cast<const int8_t*>(a.k),             \
       static_cast<const int8_t*>(a.v), a.k_scales, a.v_scales, a.scratch
 
 template <int D, int NW, int NB>
 hipError_t launch_cfg(const SplitArgs& a, hipStream_t stream) {
-  const uint32_t hblocks = (a.rows * a.group + 15u) / 16u;
-  const dim3 grid(a.splits, a.kv_heads * hblocks);
+  const uint64_t hblocks = (uint64_t(a.rows) * a.group + 15u) / 16u;
+  const uint64_t units = uint64_t(a.splits) * a.kv_heads;  // (split, kv head) pairs
+  const uint64_t groups = 8u * hblocks * ((units + 7u) / 8u);
+  if (groups > 0x7fffffffull) return hipErrorInvalidValue;
+  const dim3 grid(static_cast<uint32_t>(groups), 1u, 1u);
   if (a.page_tokens % kTileTokens == 0)
     hipLaunchKernelGGL((split_lds_kernel<D, NW, NB, true>), grid, dim3(64 * NW), 0, stream, KVB_LDS_ARGS);
   else
@@ -460,7 +656,48 @@ int lds_config(const SplitArgs& a) {
 
 }  // namespace
 
+// Tiles of a split the rows kernel holds in LDS, by dim (about 135 KiB).
+constexpr int kRowsTiles256 = 4, kRowsTiles128 = 8, kRowsTiles64 = 16;
+
+int rows_tiles(uint32_t dim) {
+  return dim == 256 ? kRowsTiles256 : (dim == 128 ? kRowsTiles128 : (dim == 64 ? kRowsTiles64 : 0));
+}
+
+// More than one head-row block and splits that start on a tile boundary and
+// fit the rows kernel's LDS.
+bool use_rows_kernel(const SplitArgs& a) {
+  if (a.rows * a.group <= 16u || a.seq_starts != nullptr) return false;
+  if (a.begin % kTileTokens != 0 || a.split_tokens % kTileTokens != 0) return false;
+  return a.split_tokens / kTileTokens <= uint32_t(rows_tiles(a.dim));
+}
+
+template <int D, int TM>
+hipError_t launch_rows(const SplitArgs& a, hipStream_t stream) {
+  const dim3 grid(a.splits, a.kv_heads);
+  if (a.page_tokens % kTileTokens == 0)
+    hipLaunchKernelGGL((split_lds_rows_kernel<D, TM, true>), grid, dim3(64 * kRowsWaves), 0, stream, KVB_LDS_ARGS);
+  else
+    hipLaunchKernelGGL((split_lds_rows_kernel<D, TM, false>), grid, dim3(64 * kRowsWaves), 0, stream, KVB_LDS_ARGS);
+  return hipGetLastError();
+}
+
+template <int D, int TM>
+hipError_t preload_rows() {
+  hipFuncAttributes attr{};
+  hipError_t e = hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_lds_rows_kernel<D, TM, true>));
+  if (e != hipSuccess) return e;
+  return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_lds_rows_kernel<D, TM, false>));
+}
+
 hipError_t launch_split_lds(const SplitArgs& a, hipStream_t stream) {
+  if (use_rows_kernel(a)) {
+    switch (a.dim) {
+      case 64: return launch_rows<64, kRowsTiles64>(a, stream);
+      case 128: return launch_rows<128, kRowsTiles128>(a, stream);
+      case 256: return launch_rows<256, kRowsTiles256>(a, stream);
+      default: break;
+    }
+  }
   const int cfg = lds_config(a);
   switch (a.dim * 100 + cfg) {
     case 12841: return launch_cfg<128, 4, 1>(a, stream);
@@ -478,6 +715,11 @@ hipError_t launch_split_lds(const SplitArgs& a, hipStream_t stream) {
 
 const char* lds_kernel_name(const SplitArgs& a) {
   static thread_local char buf[96];
+  if (use_rows_kernel(a) && rows_tiles(a.dim) > 0) {
+    std::snprintf(buf, sizeof(buf), "split_lds_rows_kernel<%u,%d,%s>", a.dim, rows_tiles(a.dim),
+                  a.page_tokens % kTileTokens == 0 ? "true" : "false");
+    return buf;
+  }
   const int cfg = lds_config(a);
   std::snprintf(buf, sizeof(buf), "split_lds_kernel<%u,%d,%d,%s>", a.dim, cfg / 10, cfg % 10,
                 a.page_tokens % kTileTokens == 0 ? "true" : "false");
@@ -494,7 +736,10 @@ hipError_t preload_lds() {
   if ((e = preload_cfg<64, 4, 2>()) != hipSuccess) return e;
   if ((e = preload_cfg<64, 4, 3>()) != hipSuccess) return e;
   if ((e = preload_cfg<256, 4, 1>()) != hipSuccess) return e;
-  return preload_cfg<256, 2, 2>();
+  if ((e = preload_cfg<256, 2, 2>()) != hipSuccess) return e;
+  if ((e = preload_rows<64, kRowsTiles64>()) != hipSuccess) return e;
+  if ((e = preload_rows<128, kRowsTiles128>()) != hipSuccess) return e;
+  return preload_rows<256, kRowsTiles256>();
 }
 
 }  // namespace kvb

@@ -74,3 +74,19 @@ def test_reference_host_tests(binary, expect):
     r = subprocess.run([path], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     assert expect in r.stdout
+
+
+def test_kernel_choice_for_the_dense_mma_geometry():
+    """rows 8 / group 6 / dim 256 / page 32 (the reference's MMA geometry): 48
+    head-rows in 3 blocks of 16.  Splits that start on a 64-token tile and fit
+    the LDS (<= 4 tiles at dim 256) run the all-blocks rows kernel, which
+    reads each split's KV once; others run the per-block LDS kernel."""
+    fake = 0x1000
+    inp = kvb.device_input(fake, fake, fake, fake, fake, fake, fake, fake)
+    s = kvb.make_shape(8, 24, 4, 256, 32, 2048, 65536, 0, 65536, 0.0625)
+    assert kvb.attention_mma_supported(s)
+    assert kvb.selected_kernel_name(s, inp, 256) == "split_lds_rows_kernel<256,4,false>"
+    assert kvb.selected_kernel_name(s, inp, 1024).startswith("split_lds_kernel<256,")        # 16 tiles per split
+    assert kvb.selected_kernel_name(s.copy(begin=32), inp, 256).startswith("split_lds_kernel<256,")  # off-tile start
+    s128 = kvb.make_shape(8, 48, 8, 128, 64, 10, 640, 64, 640, 0.0883883)
+    assert kvb.selected_kernel_name(s128, inp, 256) == "split_lds_rows_kernel<128,8,true>"
