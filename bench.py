@@ -234,6 +234,48 @@ def main():
     del probe_bufs
     log(f"stream probe: {kv_bytes} B in {probe_us:.2f} us per launch ({probe_gbs:.0f} GB/s)")
 
+    # ---- paged INT8 append (kvb_append_kv), measured before the GB-sized
+    # batched caches come and go (after them the same append has measured up
+    # to 7x slower in this process): a 4096-token prefill chunk (tokens
+    # fill the slots of randomly chosen pages in order, as a paged prefill does)
+    # and a one-token decode step into a cfg2-sized pool, fp16 sources.  Bytes
+    # moved per token and kv head: 2 x dim fp16 read, 2 x dim int8 + 8 B scales
+    # written.
+    append = None
+    if not args.no_append:
+        append = {}
+        apages = 1024
+        ak = torch.empty((apages, kvh, P, D), dtype=torch.int8, device=dev)
+        av = torch.empty((apages, kvh, D, P), dtype=torch.int8, device=dev)
+        aks = torch.empty((apages, kvh, P), dtype=torch.float32, device=dev)
+        avs = torch.empty((apages, kvh, P), dtype=torch.float32, device=dev)
+        for ntok in (4096, 1):
+            kn = torch.randn((ntok, kvh, D), device=dev).half()
+            vn = torch.randn((ntok, kvh, D), device=dev).half()
+            tok = torch.arange(ntok, device=dev)
+            slots = (torch.randperm(apages, device=dev)[tok // P] * P + tok % P).to(torch.int32)
+            ash = kvb.append_shape(ntok, kvh, D, P, apages, kvb.KVB_SRC_F16)
+
+            def acall():
+                kvb.append_kv(ash, kn, vn, slots, ak, av, aks, avs, stream=sp)
+
+            for _ in range(10):
+                acall()
+            torch.cuda.synchronize()
+            areps = max(100, args.steps // 4)
+            e0.record(stream)
+            for _ in range(areps):
+                acall()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            aus = e0.elapsed_time(e1) * 1e3 / areps
+            abytes = ntok * kvh * (2 * D * 2 + 2 * D + 8)
+            agbs = abytes / (aus * 1e-6) / 1e9
+            append[f"{ntok}_tokens"] = {"bytes_per_call": abytes, "us_per_call": round(aus, 3),
+                                        "GB/s": round(agbs, 1), "pct_of_peak": round(100.0 * agbs / HBM_PEAK_GBS, 2)}
+            log(f"append {ntok} tokens x {kvh} kv heads (fp16 source): {aus:.2f} us ({agbs:.0f} GB/s)")
+        del ak, av, aks, avs
+
     # ---- five independent cfg2 layers, each one fused
     # decode call, captured as one hipGraph step and replayed.
     five = None
@@ -371,46 +413,6 @@ def main():
             f"{100.0 * mgbs / HBM_PEAK_GBS:.1f}% of peak)")
         del mcaches, minps, msc
         torch.cuda.empty_cache()
-
-    # ---- paged INT8 append (kvb_append_kv): a 4096-token prefill chunk (tokens
-    # fill the slots of randomly chosen pages in order, as a paged prefill does)
-    # and a one-token decode step into a cfg2-sized pool, fp16 sources.  Bytes
-    # moved per token and kv head: 2 x dim fp16 read, 2 x dim int8 + 8 B scales
-    # written.
-    append = None
-    if not args.no_append:
-        append = {}
-        apages = 1024
-        ak = torch.empty((apages, kvh, P, D), dtype=torch.int8, device=dev)
-        av = torch.empty((apages, kvh, D, P), dtype=torch.int8, device=dev)
-        aks = torch.empty((apages, kvh, P), dtype=torch.float32, device=dev)
-        avs = torch.empty((apages, kvh, P), dtype=torch.float32, device=dev)
-        for ntok in (4096, 1):
-            kn = torch.randn((ntok, kvh, D), device=dev).half()
-            vn = torch.randn((ntok, kvh, D), device=dev).half()
-            tok = torch.arange(ntok, device=dev)
-            slots = (torch.randperm(apages, device=dev)[tok // P] * P + tok % P).to(torch.int32)
-            ash = kvb.append_shape(ntok, kvh, D, P, apages, kvb.KVB_SRC_F16)
-
-            def acall():
-                kvb.append_kv(ash, kn, vn, slots, ak, av, aks, avs, stream=sp)
-
-            for _ in range(10):
-                acall()
-            torch.cuda.synchronize()
-            areps = max(100, args.steps // 4)
-            e0.record(stream)
-            for _ in range(areps):
-                acall()
-            e1.record(stream)
-            torch.cuda.synchronize()
-            aus = e0.elapsed_time(e1) * 1e3 / areps
-            abytes = ntok * kvh * (2 * D * 2 + 2 * D + 8)
-            agbs = abytes / (aus * 1e-6) / 1e9
-            append[f"{ntok}_tokens"] = {"bytes_per_call": abytes, "us_per_call": round(aus, 3),
-                                        "GB/s": round(agbs, 1), "pct_of_peak": round(100.0 * agbs / HBM_PEAK_GBS, 2)}
-            log(f"append {ntok} tokens x {kvh} kv heads (fp16 source): {aus:.2f} us ({agbs:.0f} GB/s)")
-        del ak, av, aks, avs
 
     # ---- known-size kernels for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE
     if args.calibrate:
