@@ -33,7 +33,7 @@ struct MergeRowsLayout {
   static constexpr uint32_t kQT = RM * kQ;     // quads of RM row-heads
   static_assert(kQT <= kT, "merge_rows needs a thread per quad");
   static constexpr uint32_t kG = kT / kQT;     // split groups
-  static constexpr uint32_t kK = kG >= 8 ? 64u / kG : 8u;  // splits per thread per pass
+  static constexpr uint32_t kK = kG >= 4 ? 64u / kG : 16u;  // splits per thread per pass (<= 16 loads)
   static constexpr uint32_t kPS = kG * kK;     // splits per pass (<= 64)
   static_assert(kPS <= 64, "one wave computes a pass's factors");
   // LDS floats: factors [RM][kPS], (M, L, pad) [RM][4], group sums [kG][kQT] float4

@@ -76,7 +76,7 @@ bool i8_fusable(const SplitArgs& a) {
   if (a.splits <= 32 && hr * a.dim <= threads && hr <= nw) return true;
   const uint32_t quads = hs * a.dim / 4u;
   if (quads > threads) return false;
-  const uint32_t groups = threads / quads, per_pass = groups * (groups >= 8 ? 64u / groups : 8u);
+  const uint32_t groups = threads / quads, per_pass = groups * (groups >= 4 ? 64u / groups : 16u);
   return (a.splits + per_pass - 1u) / per_pass <= 2u;
 }
 

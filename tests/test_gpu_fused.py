@@ -45,7 +45,7 @@ FUSED_SHAPES = [
     (1, 32, 8, 128, 64, 8192, 5, 8192, 64, [6000]),     # 128 splits, causal cut, ragged begin
     (2, 8, 2, 128, 32, 2000, 0, 2000, 32, [1999, 700]), # 8 head-rows, 63 splits
     (1, 32, 8, 128, 64, 4096, 0, 4096, 256, None),      # four-wave groups: one 16-split merge pass
-    (1, 64, 8, 128, 64, 4096, 0, 4096, 256, [3000]),    # 8 head-rows, 16 splits: two 8-split passes
+    (1, 64, 8, 128, 64, 8192, 0, 8192, 256, [6000]),    # 8 head-rows, 32 splits: two 16-split merge passes
 ]
 
 
