@@ -411,6 +411,29 @@ def main():
                "kernel": kvb.selected_kernel_name(ms_, minps[0], 256)}
         log(f"mma geometry (launch_attention_mma): {mus:.2f} us ({mgbs:.0f} GB/s, "
             f"{100.0 * mgbs / HBM_PEAK_GBS:.1f}% of peak)")
+        # The same geometry through kvb_decode_attention with 1024-token
+        # splits: one work-group per (split, kv head) for every CU, a quarter
+        # of the partials to write and merge.
+        dst_ = 1024
+
+        def dcall(i):
+            kvb.decode_attention(ms_, minps[i % len(minps)], dst_, msc, mm_, ml_, mn_, stream=sp)
+
+        for i in range(10):
+            dcall(i)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for i in range(mreps):
+            dcall(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        dus = e0.elapsed_time(e1) * 1e3 / mreps
+        dgbs = mbytes / (dus * 1e-6) / 1e9
+        mma["decode_1024_token_splits"] = {
+            "splits": kvb.split_count(ms_, dst_), "us_per_call": round(dus, 3), "GB/s": round(dgbs, 1),
+            "pct_of_peak": round(100.0 * dgbs / HBM_PEAK_GBS, 2), "kernel": kvb.selected_kernel_name(ms_, minps[0], dst_)}
+        log(f"mma geometry (decode_attention, {dst_}-token splits): {dus:.2f} us ({dgbs:.0f} GB/s, "
+            f"{100.0 * dgbs / HBM_PEAK_GBS:.1f}% of peak)")
         del mcaches, minps, msc
         torch.cuda.empty_cache()
 

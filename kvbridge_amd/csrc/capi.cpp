@@ -182,6 +182,7 @@ static bool force_f16() {
 
 hipError_t launch_split_fast(const SplitArgs& a, hipStream_t stream) {
   if (!force_f16() && i8_supported(a)) return launch_split_i8(a, stream);
+  if (!force_f16() && i8_rows_supported(a)) return launch_split_i8_rows(a, stream);
   return launch_split_lds(a, stream);
 }
 
@@ -191,6 +192,7 @@ const char* split_kernel_name(const SplitArgs& a, bool tiled, bool int8) {
     return int8 ? "split_generic_kernel<true, false>" : "split_generic_kernel<false, false>";
   }
   if (!force_f16() && i8_supported(a)) return i8_kernel_name(a);
+  if (!force_f16() && i8_rows_supported(a)) return i8_rows_kernel_name(a);
   return lds_kernel_name(a);
 }
 
@@ -260,6 +262,7 @@ int kvb_mma_supported(const kvb_shape* s) {
 int kvb_preload_attention_reference_kernels(void) {
   hipError_t e = kvb::preload_generic();
   if (e == hipSuccess) e = kvb::preload_i8();
+  if (e == hipSuccess) e = kvb::preload_i8_rows();
   if (e == hipSuccess) e = kvb::preload_lds();
   if (e == hipSuccess) e = kvb::preload_merge();
   if (e == hipSuccess) e = kvb::preload_append();
@@ -274,6 +277,7 @@ int kvb_preload_attention_mma_kernels(void) {
   hipError_t e = hipGetDevice(&device);
   if (e != hipSuccess) return int(e);
   e = kvb::preload_lds();
+  if (e == hipSuccess) e = kvb::preload_i8_rows();
   if (e == hipSuccess) e = kvb::preload_merge();
   return int(e);
 }

@@ -57,9 +57,15 @@ hipError_t launch_split_lds(const SplitArgs& a, hipStream_t stream);  // LDS-DMA
 hipError_t launch_split_i8(const SplitArgs& a, hipStream_t stream);   // register-staged tiles, int8 MFMA
 bool i8_supported(const SplitArgs& a);  // head_rows <= 8 (<= 4 at dim 256), power-of-two pages
 bool i8_fusable(const SplitArgs& a);    // the int8 kernel can run the fused merge
+// Int8-MFMA kernel for more than 8 head-rows over short tile-aligned splits
+// (one work-group per split and kv head, the split's tiles held in LDS).
+hipError_t launch_split_i8_rows(const SplitArgs& a, hipStream_t stream);
+bool i8_rows_supported(const SplitArgs& a);  // dim 128/256, one sequence, splits of <= 8/4 whole tiles
+const char* i8_rows_kernel_name(const SplitArgs& a);
 // The MFMA split path used by the entry points: the int8-MFMA kernel where
-// i8_supported, else the f16-MFMA LDS kernel.  KVB_SPLIT_IMPL=f16 forces the
-// f16 kernel (comparisons).
+// i8_supported, else the int8-MFMA rows kernel where i8_rows_supported, else
+// the f16-MFMA LDS kernel.  KVB_SPLIT_IMPL=f16 forces the f16 kernels
+// (comparisons).
 hipError_t launch_split_fast(const SplitArgs& a, hipStream_t stream);
 hipError_t launch_split_generic(const SplitArgs& a, bool int8, hipStream_t stream);
 // Kernel instance a launch would run (diagnostics, profiles).
@@ -96,6 +102,7 @@ hipError_t launch_read_probe(const void* src, size_t bytes, uint32_t* sink, uint
 
 hipError_t preload_lds();
 hipError_t preload_i8();
+hipError_t preload_i8_rows();
 hipError_t preload_generic();
 hipError_t preload_merge();
 

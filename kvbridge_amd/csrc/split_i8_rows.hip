@@ -1,0 +1,493 @@
+// Int8-MFMA split partials for many head-rows per kv head, e.g. the
+// reference's dense rows-8 / group-6 geometry (48 head-rows per kv head, dim
+// 256; attention_shape.cpp:67-70).
+//
+// One work-group of four waves per (split, kv head) streams the split's KV
+// tiles through a two-slot LDS ring (CT tiles per slot: the tile images of
+// lds_stream.h) and every wave runs a
+// block of 16 head-rows over each tile, so the split's KV is read from HBM
+// once for all its head-rows.  While the waves compute phase p (slot p & 1),
+// the DMA of phase p + 1 is in flight; phase p + 2 is issued into the slot
+// after the barrier that ends phase p.  More than 64 head-rows (four
+// blocks) stream the split again per group of four blocks.
+//
+// Per phase, wave-local and exact in integers as in the single-block int8
+// kernel (split_i8.h):
+//  - QK: v_mfma_i32_16x16x64_i8 with the raw INT8 K codes as A and digit dg
+//    (hi, mid, lo) of the 22-bit integer 2^kq * q of the block's 16 head-rows
+//    as B; the three digit products of a (token, head-row) land in one lane.
+//  - phase maximum m_p per head-row, running maximum m = max(m, m_p); the
+//    fp32 numerators and denominators so far are rescaled by 2^(m_old - m).
+//  - PV: the weights 2^(s - m) * v_scale * 2^kp (below 2^20; kp from the
+//    phase's largest v-scale) as three 7-bit digits form B in the token order
+//    the QK result left in each lane (QK M-block mb takes tokens
+//    16q + 4mb + r, so lane (h, g) holds tokens 16g .. 16g + 15, which are
+//    its k-positions of PV), so nothing moves between lanes.  Each 16-dim block's three int32
+//    digit sums over the phase are folded into fp32 at once (2^-kp).
+// A wave owns whole head-rows and writes their partials from registers.
+// Requires splits that start on a 64-token tile (host-checked).
+#include <cstdio>
+#include <type_traits>
+
+#include "kernels.h"
+#include "device_common.h"
+#include "lds_stream.h"
+
+namespace kvb {
+namespace {
+
+using namespace lds;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 4;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// LDS reads as one asm statement each: the reads and the wait for them, so
+// the results exist only once the data is there (an asm read whose wait
+// came later could have its destination copied by the compiler before the
+// data lands), and the compiler sees no LDS load it would order after the
+// in-flight DMA of the next phase.  MFMAs issued before a batch keep
+// running while the wave waits for it.
+template <uint32_t O0, uint32_t O1, uint32_t O2, uint32_t O3>
+__device__ __forceinline__ void ds_read16x4(uint32_t a, u32x4_t& r0, u32x4_t& r1, u32x4_t& r2, u32x4_t& r3) {
+  asm volatile(
+      "ds_read_b128 %0, %4 offset:%5\n\t"
+      "ds_read_b128 %1, %4 offset:%6\n\t"
+      "ds_read_b128 %2, %4 offset:%7\n\t"
+      "ds_read_b128 %3, %4 offset:%8\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+      : "v"(a), "i"(O0), "i"(O1), "i"(O2), "i"(O3)
+      : "memory");
+}
+template <uint32_t O0, uint32_t O1>
+__device__ __forceinline__ void ds_read16x2(uint32_t a, u32x4_t& r0, u32x4_t& r1) {
+  asm volatile(
+      "ds_read_b128 %0, %2 offset:%3\n\t"
+      "ds_read_b128 %1, %2 offset:%4\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1)
+      : "v"(a), "i"(O0), "i"(O1)
+      : "memory");
+}
+template <uint32_t O0>
+__device__ __forceinline__ uint32_t ds_read4_sync(uint32_t a) {
+  uint32_t r;
+  asm volatile("ds_read_b32 %0, %1 offset:%2\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(a), "i"(O0) : "memory");
+  return r;
+}
+
+template <int D>
+struct RowsGeo {
+  static constexpr int kCT = D == 256 ? 2 : 4;  // tiles per phase (one LDS slot, about 66 KiB)
+  static constexpr uint32_t kSlot = kCT * Geo<D>::kBufBytes;
+};
+
+template <int D, bool PT>
+__global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
+    SplitArgs a, const float* __restrict__ q, const int64_t* __restrict__ qpos,
+    const int64_t* __restrict__ kpos, const uint32_t* __restrict__ table,
+    const int8_t* __restrict__ kdata, const int8_t* __restrict__ vdata,
+    const float* __restrict__ kscale, const float* __restrict__ vscale, float* __restrict__ scratch) {
+  using G = Geo<D>;
+  constexpr int CT = RowsGeo<D>::kCT;
+  constexpr uint32_t kSlot = RowsGeo<D>::kSlot;
+  constexpr int KS = D / 64;  // K-steps of QK
+  constexpr int MB = D / 16;  // 16-dim blocks of PV
+  constexpr uint32_t W = D + 2;
+  static_assert(CT <= kWaves, "one tile per wave per phase");
+  static_assert(G::kLoadsPerTile <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kSlot];
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t n = lane & 15u, g = lane >> 4;
+  const uint32_t split = blockIdx.x, kv = blockIdx.y;
+  const uint32_t head_rows = a.rows * a.group, hblocks = (head_rows + 15u) / 16u;
+  const uint32_t rounds = (hblocks + kWaves - 1u) / kWaves;
+
+  const uint64_t s0_64 = uint64_t(a.begin) + uint64_t(split) * a.split_tokens;
+  const uint32_t s0 = s0_64 < a.end ? uint32_t(s0_64) : a.end;
+  const uint32_t s1 = uint64_t(s0) + a.split_tokens < a.end ? s0 + a.split_tokens : a.end;
+  const uint32_t k_first = s0 / kTileTokens;
+  const uint32_t ntiles = s1 > s0 ? (s1 - 1u) / kTileTokens + 1u - k_first : 0u;
+  const uint32_t nphase = (ntiles + CT - 1u) / CT;
+
+  Ctx c;
+  PtCtx pc;
+  if (ntiles > 0) {
+    c.k = kdata;
+    c.v = vdata;
+    c.ks = kscale;
+    c.vs = vscale;
+    c.table = table;
+    c.kv = kv;
+    c.kv_heads = a.kv_heads;
+    c.P = a.page_tokens;
+    c.pages = a.pages;
+    c.lp_lo = s0 / a.page_tokens;
+    c.lp_hi = (s1 - 1u) / a.page_tokens;
+    c.lane = lane;
+    const uint32_t lp = c.lp_lo + lane;
+    c.ptab = lp <= c.lp_hi ? table[lp] : 0u;
+    if constexpr (PT) {
+      const uint32_t kv_bytes = a.pages * a.kv_heads * a.page_tokens * uint32_t(D);
+      const uint32_t sc_bytes = a.pages * a.kv_heads * a.page_tokens * 4u;
+      pt_init<D>(pc, kdata, vdata, kscale, vscale, kv_bytes, sc_bytes, a.page_tokens, lane);
+    }
+  }
+  // Tile p * CT + j of the split goes to slot p & 1, position j, by wave j.
+  auto issued = [&](uint32_t p) -> bool { return wave < uint32_t(CT) && p * CT + wave < ntiles; };
+  auto issue = [&](uint32_t p) {
+    if (!issued(p)) return;
+    uint8_t* const buf = smem + (p & 1u) * kSlot + wave * G::kBufBytes;
+    const uint32_t k = k_first + p * CT + wave;
+    if constexpr (PT) {
+      const uint32_t lp = k * kTileTokens / a.page_tokens;
+      const uint32_t rel = lp - c.lp_lo;
+      uint32_t phys = rel < 64u ? __builtin_amdgcn_readlane(c.ptab, rel) : table[lp];
+      phys = phys < a.pages ? phys : a.pages - 1u;
+      pt_issue<D>(pc, phys * a.kv_heads + kv, k * kTileTokens - lp * a.page_tokens, a.page_tokens, buf);
+    } else {
+      issue_tile<D>(c, k, buf);
+    }
+  };
+
+  // Per-lane LDS offsets inside a tile image.  Row i of QK M-block mb is
+  // token 16 * (i >> 2) + 4mb + (i & 3), so the QK result leaves tokens
+  // 16g .. 16g + 15 of head-row h in lane (h, g) and the PV A operand of lane
+  // (d, g) is V[d][16g .. 16g + 15], one 16-byte read.  K: lane (n, g) reads
+  // row r = 16 * (n >> 2) + (n & 3) + 4mb, chunk 4s + g, at position
+  // (4s + g) ^ swz_k(r) (swz_k(r) does not depend on mb).  V: dim row
+  // d = 16mb + n, token group g at position g ^ swz_v(d) (swz_v(d) = swz_v(n)).
+  const uint32_t lds_base = lds_addr(smem);
+  uint32_t koff[KS];
+  {
+    const uint32_t r0 = 16u * (n >> 2) + (n & 3u);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) koff[s] = r0 * D + 16u * ((4u * s + g) ^ swz_k<D>(r0));
+  }
+  const uint32_t voff = G::kKBytes + 64u * n + 16u * (g ^ swz_v(n));
+  const uint32_t soff = G::kKBytes + G::kVBytes + 64u * g;  // k-scales of tokens 16g .. ; v-scales at +256
+  const uint32_t vmoff = G::kKBytes + G::kVBytes + 256u + 4u * lane;
+
+  for (uint32_t round = 0; round < rounds; ++round) {
+    const uint32_t hblock = wave + kWaves * round;
+    const bool has = hblock < hblocks;  // wave-uniform
+    if (nphase > 0) issue(0);
+    if (nphase > 1) issue(1);
+
+    // ---- block prologue: visibility, Q digits
+    const uint32_t hr = hblock * 16u + n;
+    const bool hvalid = hr < head_rows;
+    const uint32_t row = hvalid ? hr / a.group : 0u;
+    const uint32_t head = kv * a.group + (hvalid ? hr % a.group : 0u);
+    uint32_t e_h = s0, e_min = s0, e_max = s0;
+    i32x4 qd[3][KS];
+    float cs = 0.f;
+    if (has) {
+      if (s1 > s0) {
+        const uint32_t r_lo = hblock * 16u / a.group;
+        const uint32_t r_hi = (hblock * 16u + 15u < head_rows ? hblock * 16u + 15u : head_rows - 1u) / a.group;
+        const int64_t klast = kpos[s1 - 1u];
+        bool all_visible = true;
+        for (uint32_t r = r_lo; r <= r_hi; ++r) all_visible &= klast <= qpos[r];
+        if (all_visible) {
+          e_h = s1;
+        } else {
+          for (uint32_t r = r_lo; r <= r_hi; ++r) {
+            const uint32_t e = visible_end(kpos, s0, s1, qpos[r], lane);
+            if (row == r) e_h = e;
+          }
+        }
+        if (!hvalid) e_h = s0;
+      }
+      uint32_t lo = hvalid ? e_h : 0xffffffffu, hi = e_h;
+#define KVB_ROW_RED(N)                                                                                 \
+  {                                                                                                    \
+    const uint32_t o1 = uint32_t(__builtin_amdgcn_update_dpp(0, int(lo), 0x120 + N, 0xF, 0xF, false)); \
+    const uint32_t o2 = uint32_t(__builtin_amdgcn_update_dpp(0, int(hi), 0x120 + N, 0xF, 0xF, false)); \
+    lo = o1 < lo ? o1 : lo;                                                                            \
+    hi = o2 > hi ? o2 : hi;                                                                            \
+  }
+      KVB_ROW_RED(8) KVB_ROW_RED(4) KVB_ROW_RED(2) KVB_ROW_RED(1)
+#undef KVB_ROW_RED
+      e_min = __builtin_amdgcn_readfirstlane(lo);
+      e_max = __builtin_amdgcn_readfirstlane(hi);
+
+      // Q digits (B of QK): lane (h, g) holds dims 64s + 16g .. +15 of
+      // head-row h; digit dg of the 22-bit integer 2^kq * q in qd[dg].
+      float qv[KS][16];
+      if (hvalid) {
+        const float* qp = q + (size_t(row) * a.q_heads + head) * D + 16u * g;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float4 x = reinterpret_cast<const float4*>(qp + 64 * s)[j];
+            qv[s][4 * j] = x.x;
+            qv[s][4 * j + 1] = x.y;
+            qv[s][4 * j + 2] = x.z;
+            qv[s][4 * j + 3] = x.w;
+          }
+      } else {
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) qv[s][i] = 0.f;
+      }
+      float amax = 0.f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(qv[s][i]));
+      amax = rows_max(amax);
+      int kq = 0;
+      if (amax > 0.f) {
+        kq = 21 - __builtin_amdgcn_frexp_expf(amax);
+        kq = kq < -100 ? -100 : (kq > 100 ? 100 : kq);
+      }
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        uint32_t w[3][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[0][i] = w[1][i] = w[2][i] = 0u;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int qi = int(__builtin_rintf(__builtin_amdgcn_ldexpf(qv[s][i], kq)));  // |qi| <= 2^21
+          const int lo8 = __builtin_amdgcn_sbfe(qi, 0, 8);
+          const int r1 = (qi - lo8) >> 8;
+          const int mid8 = __builtin_amdgcn_sbfe(r1, 0, 8);
+          const int hi8 = (r1 - mid8) >> 8;
+          w[0][i / 4] |= (uint32_t(hi8) & 0xffu) << (8 * (i % 4));
+          w[1][i / 4] |= (uint32_t(mid8) & 0xffu) << (8 * (i % 4));
+          w[2][i / 4] |= (uint32_t(lo8) & 0xffu) << (8 * (i % 4));
+        }
+#pragma unroll
+        for (int dg = 0; dg < 3; ++dg) qd[dg][s] = i32x4{int(w[dg][0]), int(w[dg][1]), int(w[dg][2]), int(w[dg][3])};
+      }
+      cs = __builtin_amdgcn_ldexpf(a.scale, -kq) * kLog2e;  // score factor, log2 units
+    }
+    const uint32_t nvis = has && e_max > s0 ? (e_max - 1u) / kTileTokens + 1u - k_first : 0u;  // tiles
+
+    float m_run = neg_inf(), l_run = 0.f;  // per lane: head-row h's running max (log2) and partial sum
+    f32x4 acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (uint32_t p = 0; p < nphase; ++p) {
+      if (issued(p + 1u)) wait_vm<G::kLoadsPerTile>();
+      else wait_vm<0>();
+      __syncthreads();
+      const uint32_t tp = p * CT;  // first tile of the phase (split-relative)
+      if (tp < nvis) {
+        // LDS addresses of the slot (tile j adds j * kBufBytes as an immediate).
+        const uint32_t pb = lds_base + (p & 1u) * kSlot;
+        uint32_t ka[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) ka[s] = pb + koff[s];
+        const uint32_t va = pb + voff, sa = pb + soff, vma = pb + vmoff;
+
+        // ---- QK: scores of the phase's tiles, lane (h, g): tokens 16g + 4mb + e
+        float sc[CT][16];
+        float mx = neg_inf();
+        static_for<0, CT>([&](auto jc) __attribute__((always_inline)) {
+          constexpr uint32_t j = decltype(jc)::value;
+          constexpr uint32_t TB = j * G::kBufBytes;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sc[j][i] = neg_inf();
+          if (tp + j >= nvis) return;
+          const uint32_t t0 = (k_first + tp + j) * kTileTokens;
+          u32x4_t ks[4];
+          ds_read16x4<TB, TB + 16u, TB + 32u, TB + 48u>(sa, ks[0], ks[1], ks[2], ks[3]);
+          i32x4 cq[3][4];
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int dg = 0; dg < 3; ++dg) cq[dg][mb] = i32x4{0, 0, 0, 0};
+          static_for<0, KS>([&](auto sc_) __attribute__((always_inline)) {
+            constexpr uint32_t s = decltype(sc_)::value;
+            u32x4_t kr[4];
+            ds_read16x4<TB, TB + 4u * D, TB + 8u * D, TB + 12u * D>(ka[s], kr[0], kr[1], kr[2], kr[3]);
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) {
+              const i32x4 av = {int(kr[mb][0]), int(kr[mb][1]), int(kr[mb][2]), int(kr[mb][3])};
+#pragma unroll
+              for (int dg = 0; dg < 3; ++dg)
+                cq[dg][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, qd[dg][s], cq[dg][mb], 0, 0, 0);
+            }
+          });
+          const bool full = t0 + kTileTokens <= e_min;  // every head-row of the block sees the whole tile
+          const uint32_t vis = e_h > t0 ? (e_h - t0 < kTileTokens ? e_h - t0 : kTileTokens) : 0u;
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int hi2 = cq[0][mb][e] * 256 + cq[1][mb][e];  // |.| < 2^29
+              float s2 = fmaf(float(hi2), 256.f, float(cq[2][mb][e])) * (__uint_as_float(ks[mb][e]) * cs);
+              if (!full) s2 = 16u * g + 4u * mb + e < vis ? s2 : neg_inf();
+              sc[j][4 * mb + e] = s2;
+              mx = fmaxf(mx, s2);
+            }
+          }
+        });
+
+        // ---- v-scales of the phase, running maximum, weight exponent kp
+        u32x4_t vsr[CT][4];
+        float vm = 0.f;
+        static_for<0, CT>([&](auto jc) __attribute__((always_inline)) {
+          constexpr uint32_t j = decltype(jc)::value;
+          constexpr uint32_t TB = j * G::kBufBytes;
+          if (tp + j >= nvis) return;
+          ds_read16x4<TB + 256u, TB + 272u, TB + 288u, TB + 304u>(sa, vsr[j][0], vsr[j][1], vsr[j][2], vsr[j][3]);
+          const float v = __uint_as_float(ds_read4_sync<TB>(vma));
+          const uint32_t t0 = (k_first + tp + j) * kTileTokens;
+          vm = t0 + lane < e_max ? fmaxf(vm, fabsf(v)) : vm;
+        });
+        const float m_new = fmaxf(m_run, rows_max(mx));
+        const float vmax = wave_max(vm);
+        int kp = 0;
+        if (vmax > 0.f) {
+          kp = 20 - __builtin_amdgcn_frexp_expf(vmax);
+          kp = kp < -100 ? -100 : (kp > 100 ? 100 : kp);
+        }
+        const float f = m_run == neg_inf() ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+        if (__ballot(f != 1.f) != 0) {
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) acc[mb] *= f;
+        }
+        const float mu = (m_new == neg_inf() ? 0.f : m_new) - float(kp);  // 2^(s - mu) = w * 2^kp
+        m_run = m_new;
+
+        // ---- weights as three 7-bit digits (B of PV), k-position = token 16g + 4mb + e
+        i32x4 bd[CT][3];
+        float lw = 0.f;
+        static_for<0, CT>([&](auto jc) __attribute__((always_inline)) {
+          constexpr uint32_t j = decltype(jc)::value;
+          if (tp + j >= nvis) return;
+          const uint32_t t0 = (k_first + tp + j) * kTileTokens;
+          const bool vfull = t0 + kTileTokens <= e_max;  // no token past the block's last visible one
+          const uint32_t vlim = e_max - t0;
+          uint32_t bw[3][4];
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb) {
+            bw[0][mb] = bw[1][mb] = bw[2][mb] = 0u;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float w = __builtin_amdgcn_exp2f(sc[j][4 * mb + e] - mu);  // w * 2^kp
+              lw += w;
+              float vsl = __uint_as_float(vsr[j][mb][e]);
+              if (!vfull) vsl = 16u * g + 4u * mb + e < vlim ? vsl : 0.f;  // slots past the data
+              const int pint = int(__builtin_rintf(w * vsl));
+              bw[0][mb] |= (uint32_t(pint >> 14) & 0xffu) << (8 * e);
+              bw[1][mb] |= ((uint32_t(pint) >> 7) & 0x7fu) << (8 * e);
+              bw[2][mb] |= (uint32_t(pint) & 0x7fu) << (8 * e);
+            }
+          }
+#pragma unroll
+          for (int dg = 0; dg < 3; ++dg)
+            bd[j][dg] = i32x4{int(bw[dg][0]), int(bw[dg][1]), int(bw[dg][2]), int(bw[dg][3])};
+        });
+        const float inv = __builtin_amdgcn_ldexpf(1.f, -kp);
+        l_run = fmaf(lw, inv, l_run * f);
+
+        // ---- PV per 16-dim block: A = V[16mb + n][16g .. 16g + 15], one read per tile
+        static_for<0, MB>([&](auto mc) __attribute__((always_inline)) {
+          constexpr uint32_t mb = decltype(mc)::value;
+          u32x4_t vr[CT];
+          if constexpr (CT == 2) {
+            ds_read16x2<1024u * mb, G::kBufBytes + 1024u * mb>(va, vr[0], vr[1]);
+          } else {
+            ds_read16x4<1024u * mb, G::kBufBytes + 1024u * mb, 2u * G::kBufBytes + 1024u * mb,
+                        3u * G::kBufBytes + 1024u * mb>(va, vr[0], vr[1], vr[2], vr[3]);
+          }
+          i32x4 cv[3] = {i32x4{0, 0, 0, 0}, i32x4{0, 0, 0, 0}, i32x4{0, 0, 0, 0}};
+          static_for<0, CT>([&](auto jc) __attribute__((always_inline)) {
+            constexpr uint32_t j = decltype(jc)::value;
+            if (tp + j >= nvis) return;
+            const i32x4 av = {int(vr[j][0]), int(vr[j][1]), int(vr[j][2]), int(vr[j][3])};
+#pragma unroll
+            for (int dg = 0; dg < 3; ++dg) cv[dg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bd[j][dg], cv[dg], 0, 0, 0);
+          });
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int hi2 = cv[0][e] * 128 + cv[1][e];  // |.| < 2^29
+            acc[mb][e] = fmaf(fmaf(float(hi2), 128.f, float(cv[2][e])), inv, acc[mb][e]);
+          }
+        });
+      }
+      __syncthreads();  // slot p & 1 is free
+      if (p + 2u < nphase) issue(p + 2u);
+    }
+
+    // ---- this block's partials from the registers (lane (h, g): dims 16mb + 4g + e)
+    if (has) {
+      const float l_h = rows_sum(l_run);
+      if (hvalid) {
+        float* const dst = scratch + ((size_t(row) * a.q_heads + head) * a.splits + split) * W;
+        if (g == 0) {
+          dst[0] = m_run * kLn2;
+          dst[1] = l_h;
+        }
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dst[2 + 16 * mb + 4 * g + e] = acc[mb][e];
+      }
+    }
+  }
+}
+
+#define KVB_I8R_ARGS                                                                             \
+  a, a.q, a.q_positions, a.k_positions, a.page_table, static_cast<const int8_t*>(a.k),             \
+      static_cast<const int8_t*>(a.v), a.k_scales, a.v_scales, a.scratch
+
+template <int D>
+hipError_t launch_dim(const SplitArgs& a, hipStream_t stream) {
+  const dim3 grid(a.splits, a.kv_heads);
+  if (a.page_tokens % kTileTokens == 0)
+    hipLaunchKernelGGL((split_i8_rows_kernel<D, true>), grid, dim3(64 * kWaves), 0, stream, KVB_I8R_ARGS);
+  else
+    hipLaunchKernelGGL((split_i8_rows_kernel<D, false>), grid, dim3(64 * kWaves), 0, stream, KVB_I8R_ARGS);
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t preload_dim() {
+  hipFuncAttributes attr{};
+  hipError_t e = hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_i8_rows_kernel<D, true>));
+  if (e != hipSuccess) return e;
+  return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_i8_rows_kernel<D, false>));
+}
+
+}  // namespace
+
+// More than 8 head-rows (the single-block int8 kernel's limit), dim 128 or
+// 256, one sequence, splits that start on a 64-token tile.
+bool i8_rows_supported(const SplitArgs& a) {
+  if (a.rows * a.group <= 8u || a.seq_starts != nullptr) return false;
+  if (a.dim != 128 && a.dim != 256) return false;
+  return a.begin % kTileTokens == 0 && a.split_tokens % kTileTokens == 0;
+}
+
+hipError_t launch_split_i8_rows(const SplitArgs& a, hipStream_t stream) {
+  switch (a.dim) {
+    case 128: return launch_dim<128>(a, stream);
+    case 256: return launch_dim<256>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+const char* i8_rows_kernel_name(const SplitArgs& a) {
+  static thread_local char buf[96];
+  std::snprintf(buf, sizeof(buf), "split_i8_rows_kernel<%u,%s>", a.dim,
+                a.page_tokens % kTileTokens == 0 ? "true" : "false");
+  return buf;
+}
+
+hipError_t preload_i8_rows() {
+  const hipError_t e = preload_dim<128>();
+  if (e != hipSuccess) return e;
+  return preload_dim<256>();
+}
+
+}  // namespace kvb

@@ -78,15 +78,19 @@ def test_reference_host_tests(binary, expect):
 
 def test_kernel_choice_for_the_dense_mma_geometry():
     """rows 8 / group 6 / dim 256 / page 32 (the reference's MMA geometry): 48
-    head-rows in 3 blocks of 16.  Splits that start on a 64-token tile and fit
-    the LDS (<= 4 tiles at dim 256) run the all-blocks rows kernel, which
-    reads each split's KV once; others run the per-block LDS kernel."""
+    head-rows in 3 blocks of 16.  Splits that start on a 64-token tile run the
+    int8-MFMA rows kernel, which streams each split's KV once for every
+    head-row block; an off-tile start runs the per-block LDS kernel.
+    KVB_SPLIT_IMPL=f16 would pick the f16 kernels."""
     fake = 0x1000
     inp = kvb.device_input(fake, fake, fake, fake, fake, fake, fake, fake)
     s = kvb.make_shape(8, 24, 4, 256, 32, 2048, 65536, 0, 65536, 0.0625)
     assert kvb.attention_mma_supported(s)
-    assert kvb.selected_kernel_name(s, inp, 256) == "split_lds_rows_kernel<256,4,false>"
-    assert kvb.selected_kernel_name(s, inp, 1024).startswith("split_lds_kernel<256,")        # 16 tiles per split
+    assert kvb.selected_kernel_name(s, inp, 256) == "split_i8_rows_kernel<256,false>"
+    assert kvb.selected_kernel_name(s, inp, 1024) == "split_i8_rows_kernel<256,false>"
+    assert kvb.selected_kernel_name(s, inp, 1000).startswith("split_lds_kernel<256,")  # off-tile split size
     assert kvb.selected_kernel_name(s.copy(begin=32), inp, 256).startswith("split_lds_kernel<256,")  # off-tile start
     s128 = kvb.make_shape(8, 48, 8, 128, 64, 10, 640, 64, 640, 0.0883883)
-    assert kvb.selected_kernel_name(s128, inp, 256) == "split_lds_rows_kernel<128,8,true>"
+    assert kvb.selected_kernel_name(s128, inp, 256) == "split_i8_rows_kernel<128,true>"
+    s64 = kvb.make_shape(8, 48, 8, 64, 64, 10, 640, 64, 640, 0.125)
+    assert kvb.selected_kernel_name(s64, inp, 256).startswith("split_lds_rows_kernel<64,")  # dim 64: f16 rows kernel

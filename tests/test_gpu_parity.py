@@ -5,6 +5,8 @@ output n/l, identical visibility, and the empty-row convention (m = -inf,
 l = 0, n = 0).  The reference's stricter per-element gate
 |a - r| <= 3e-6 + 5e-5|r| (examples/attention_bench.cu:127) is printed.
 """
+import zlib
+
 import numpy as np
 import pytest
 
@@ -116,6 +118,54 @@ def test_tiled_shapes(gpu, cfg):
     check_against_oracle(case, mln, f"decode split_tokens={st}", ref)
     mln2, _ = dc.run_reference_api()
     check_against_oracle(case, mln2, "launch_attention", ref)
+
+
+I8_ROWS_SHAPES = [
+    # rows, q_heads, kv_heads, dim, P, tokens, begin, end, split_tokens, query positions, outliers
+    (8, 24, 4, 256, 32, 2048, 0, 2048, 256, "causal", 0.0),    # the dense rows-8 / group-6 geometry
+    (4, 24, 4, 256, 32, 1000, 0, 1000, 256, "spread", 0.0),    # 24 head-rows: second block half empty
+    (3, 32, 2, 128, 16, 900, 128, 900, 512, "spread", 0.02),   # 48 head-rows, 16-token pages, 8-tile splits
+    (5, 24, 8, 256, 64, 700, 0, 700, 192, "masked", 0.0),      # 15 head-rows, page-tile path, masked rows
+    (2, 48, 4, 128, 64, 1536, 64, 1500, 448, "causal", 0.05),  # 24 head-rows, 7-tile splits, ragged end
+    (8, 96, 4, 128, 32, 3000, 0, 3000, 2048, "spread", 0.0),   # 192 head-rows: three streams of 4 blocks
+    (8, 24, 4, 256, 32, 4096, 0, 4000, 1344, "causal", 0.0),   # dense geometry, 21-tile splits (odd phase)
+]
+
+
+def _query_positions(kind, rows, begin, end, rng):
+    if kind == "causal":
+        return None  # rows end at tokens - rows + i
+    if kind == "spread":  # one row before the range, the others cut anywhere inside it
+        q = rng.integers(begin, end, size=rows).astype(np.int64)
+        q[0] = begin - 1
+        return q
+    q = rng.integers(begin, end, size=rows).astype(np.int64)  # "masked": every other row sees nothing
+    q[::2] = -1
+    return q
+
+
+@pytest.mark.parametrize("cfg", I8_ROWS_SHAPES)
+def test_i8_rows_kernel_shapes(gpu, cfg):
+    """More than 8 head-rows over short tile-aligned splits run the int8-MFMA
+    rows kernel (all head-row blocks of a kv head over one LDS copy of the
+    split); per-row causal cuts, fully masked rows and outlier tokens."""
+    rows, qh, kvh, d, p, t, b, e, st, kind, outl = cfg
+    seed = zlib.crc32(repr(cfg).encode()) & 0xFFFF  # str hashes vary per process
+    qpos = _query_positions(kind, rows, b, e, np.random.default_rng(seed))
+    case = W.synth_case(rows, qh, kvh, d, p, t, seed=seed, begin=b, end=e, qpos=qpos, outlier_frac=outl)
+    name = kvb.selected_kernel_name(case.shape, kvb.device_input(*([0x1000] * 8)), st)
+    log(f"i8 rows shape={case.shape.as_tuple()} split_tokens={st} qpos={kind} kernel={name}")
+    assert name.startswith("split_i8_rows_kernel<"), name
+    dc = DeviceCase(case)
+    ref = O.fp64(case, threads=8)
+    mln, _, _ = dc.run_decode(st)
+    check_against_oracle(case, mln, f"decode split_tokens={st}", ref)
+    mma = kvb.attention_mma_supported(case.shape)
+    mln2, _ = dc.run_reference_api(mma=mma)
+    check_against_oracle(case, mln2, "launch_attention_mma" if mma else "launch_attention", ref)
+    mln3, _, _ = dc.run_decode(st)
+    for x, y in zip(mln, mln3):  # bitwise repeatable
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
 
 
 GENERIC_SHAPES = [
