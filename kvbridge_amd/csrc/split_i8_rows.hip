@@ -318,17 +318,23 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
           });
           const bool full = t0 + kTileTokens <= e_min;  // every head-row of the block sees the whole tile
           const uint32_t vis = e_h > t0 ? (e_h - t0 < kTileTokens ? e_h - t0 : kTileTokens) : 0u;
+          // Masking only on the tiles that need it (separate code paths).
+          auto scores = [&](auto maskc) __attribute__((always_inline)) {
+            constexpr bool MASK = decltype(maskc)::value;
 #pragma unroll
-          for (int mb = 0; mb < 4; ++mb) {
+            for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int hi2 = cq[0][mb][e] * 256 + cq[1][mb][e];  // |.| < 2^29
-              float s2 = fmaf(float(hi2), 256.f, float(cq[2][mb][e])) * (__uint_as_float(ks[mb][e]) * cs);
-              if (!full) s2 = 16u * g + 4u * mb + e < vis ? s2 : neg_inf();
-              sc[j][4 * mb + e] = s2;
-              mx = fmaxf(mx, s2);
+              for (int e = 0; e < 4; ++e) {
+                const int hi2 = cq[0][mb][e] * 256 + cq[1][mb][e];  // |.| < 2^29
+                float s2 = fmaf(float(hi2), 256.f, float(cq[2][mb][e])) * (__uint_as_float(ks[mb][e]) * cs);
+                if constexpr (MASK) s2 = 16u * g + 4u * mb + e < vis ? s2 : neg_inf();
+                sc[j][4 * mb + e] = s2;
+                mx = fmaxf(mx, s2);
+              }
             }
-          }
+          };
+          if (full) scores(std::false_type{});
+          else scores(std::true_type{});
         });
 
         // ---- v-scales of the phase, running maximum, weight exponent kp
@@ -368,21 +374,26 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
           const bool vfull = t0 + kTileTokens <= e_max;  // no token past the block's last visible one
           const uint32_t vlim = e_max - t0;
           uint32_t bw[3][4];
+          auto digits = [&](auto maskc) __attribute__((always_inline)) {
+            constexpr bool MASK = decltype(maskc)::value;
 #pragma unroll
-          for (int mb = 0; mb < 4; ++mb) {
-            bw[0][mb] = bw[1][mb] = bw[2][mb] = 0u;
+            for (int mb = 0; mb < 4; ++mb) {
+              bw[0][mb] = bw[1][mb] = bw[2][mb] = 0u;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float w = __builtin_amdgcn_exp2f(sc[j][4 * mb + e] - mu);  // w * 2^kp
-              lw += w;
-              float vsl = __uint_as_float(vsr[j][mb][e]);
-              if (!vfull) vsl = 16u * g + 4u * mb + e < vlim ? vsl : 0.f;  // slots past the data
-              const int pint = int(__builtin_rintf(w * vsl));
-              bw[0][mb] |= (uint32_t(pint >> 14) & 0xffu) << (8 * e);
-              bw[1][mb] |= ((uint32_t(pint) >> 7) & 0x7fu) << (8 * e);
-              bw[2][mb] |= (uint32_t(pint) & 0x7fu) << (8 * e);
+              for (int e = 0; e < 4; ++e) {
+                const float w = __builtin_amdgcn_exp2f(sc[j][4 * mb + e] - mu);  // w * 2^kp
+                lw += w;
+                float vsl = __uint_as_float(vsr[j][mb][e]);
+                if constexpr (MASK) vsl = 16u * g + 4u * mb + e < vlim ? vsl : 0.f;  // slots past the data
+                const int pint = int(__builtin_rintf(w * vsl));
+                bw[0][mb] |= (uint32_t(pint >> 14) & 0xffu) << (8 * e);
+                bw[1][mb] |= ((uint32_t(pint) >> 7) & 0x7fu) << (8 * e);
+                bw[2][mb] |= (uint32_t(pint) & 0x7fu) << (8 * e);
+              }
             }
-          }
+          };
+          if (vfull) digits(std::false_type{});
+          else digits(std::true_type{});
 #pragma unroll
           for (int dg = 0; dg < 3; ++dg)
             bd[j][dg] = i32x4{int(bw[dg][0]), int(bw[dg][1]), int(bw[dg][2]), int(bw[dg][3])};
