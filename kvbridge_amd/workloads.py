@@ -285,6 +285,12 @@ def cfg3_lengths(seed=0x4B56423):
     return [int(x) for x in np.random.default_rng(seed).integers(1024, 32768, size=16, endpoint=True)]
 
 
-CFG3 = dict(rows=1, q_heads=32, kv_heads=8, dim=128, page_tokens=64, split_tokens=2048)
+# configs[2] leaves the chunk count per sequence free ("chosen from its
+# length"): ceil(length / 5120) chunks puts the batch's 57 chunks x 8 kv heads
+# (456 work-groups) in one round of two work-groups per CU.  Measured on
+# MI355X (split + merge, µs): 1024: 134, 1536: 101.5, 2048: 116.7, 3072: 99.5,
+# 4096: 129, 4608: 101, 5120: 90.9, 6144: 95.5 -- a second, partly filled
+# round of work-groups costs up to a third more.
+CFG3 = dict(rows=1, q_heads=32, kv_heads=8, dim=128, page_tokens=64, split_tokens=5120)
 CFG4 = dict(rows=1, q_heads=64, kv_heads=8, dim=128, page_tokens=64, split_tokens=2048,
             lengths=[131072] * 4, outlier_frac=0.01)
