@@ -190,6 +190,112 @@ __global__ __launch_bounds__(64 * kWaves) void append_tile_kernel(AppendArgs a) 
   }
 }
 
+// append_stream_kernel (prefill-sized appends from 16-byte aligned rows, dim
+// 64/128/256): one work-group of four waves per (64 new tokens, kv head).
+// Wave w loads tokens 16w .. 16w + 15 row-major (LPR lanes per row, 16 bytes
+// each: one coalesced pass, every row read once), the row absmax is an xor
+// shuffle over those lanes, and K codes go out as each lane's contiguous
+// 16 / sizeof(T) bytes of the token's row.  V codes are transposed through
+// LDS ([dim][64 tokens]) and stored 16 tokens per 16-byte store where those
+// 16 tokens fill 16 consecutive slots of one page starting on a 16-slot
+// boundary (a prefill chunk); any other group of 16 is stored byte by byte.
+template <class T, int D>
+__global__ __launch_bounds__(64 * kWaves) void append_stream_kernel(AppendArgs a) {
+  constexpr uint32_t EPL = 16 / sizeof(T);  // elements per lane per load
+  constexpr uint32_t LPR = D / EPL;         // lanes per row
+  static_assert(LPR >= 4 && LPR <= 64 && 64 % LPR == 0, "row split");
+  constexpr uint32_t RPL = 64 / LPR;        // rows per wave-load
+  __shared__ __attribute__((aligned(16))) uint8_t vt[D * 64];  // V codes [d][token]
+  __shared__ uint32_t ids[64];
+  __shared__ uint32_t grp_ok[4];
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t kv = blockIdx.y, t0 = blockIdx.x * 64u;
+  const uint32_t P = a.page_tokens, cap = a.pages * a.page_tokens;
+  if (wave == 0) {
+    const uint32_t t = t0 + lane;
+    const uint32_t id = t < a.tokens ? a.slots[t] : cap;
+    ids[lane] = id;
+    const uint32_t id0 = __shfl(id, int(lane & ~15u));
+    const bool ok = id < cap && id == id0 + (lane & 15u) && id0 % 16u == 0u;
+    const uint64_t b = __ballot(ok);
+    if ((lane & 15u) == 0u) grp_ok[lane >> 4] = ((b >> (lane & ~15u)) & 0xffffull) == 0xffffull ? 1u : 0u;
+  }
+  __syncthreads();
+  const uint32_t sub = lane % LPR, e0 = sub * EPL;
+#pragma unroll
+  for (uint32_t i = 0; i < 16u / RPL; ++i) {
+    const uint32_t r = 16u * wave + RPL * i + lane / LPR;  // token of the tile
+    const uint32_t t = t0 + r;
+    const uint32_t id = ids[r];
+    const bool live = t < a.tokens;
+    float xk[EPL], xv[EPL];
+    if (live) {  // one 16-byte load of each row slice
+      const u32x4 wk = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k_new) + size_t(t) * a.k_stride +
+                                                       size_t(kv) * D + e0);
+      const u32x4 wv = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v_new) + size_t(t) * a.v_stride +
+                                                       size_t(kv) * D + e0);
+      const T* ek = reinterpret_cast<const T*>(&wk);
+      const T* ev = reinterpret_cast<const T*>(&wv);
+#pragma unroll
+      for (uint32_t e = 0; e < EPL; ++e) {
+        xk[e] = to_f32(ek[e]);
+        xv[e] = to_f32(ev[e]);
+      }
+    } else {
+#pragma unroll
+      for (uint32_t e = 0; e < EPL; ++e) xk[e] = xv[e] = 0.f;
+    }
+    float ka = 0.f, va = 0.f;
+#pragma unroll
+    for (uint32_t e = 0; e < EPL; ++e) {
+      ka = fmaxf(ka, fabsf(xk[e]));
+      va = fmaxf(va, fabsf(xv[e]));
+    }
+#pragma unroll
+    for (uint32_t o = 1; o < LPR; o <<= 1) {
+      ka = fmaxf(ka, __shfl_xor(ka, int(o)));
+      va = fmaxf(va, __shfl_xor(va, int(o)));
+    }
+    const float ks = ka == 0.f ? 1.f : ka / 127.f;
+    const float vs = va == 0.f ? 1.f : va / 127.f;
+    uint32_t kw[EPL / 4];
+#pragma unroll
+    for (uint32_t e = 0; e < EPL / 4; ++e) kw[e] = 0u;
+#pragma unroll
+    for (uint32_t e = 0; e < EPL; ++e) {
+      kw[e / 4] |= uint32_t(uint8_t(quantize(xk[e], ks))) << (8 * (e % 4));
+      vt[(e0 + e) * 64u + r] = uint8_t(quantize(xv[e], vs));
+    }
+    if (id < cap) {
+      const size_t row = (size_t(id / P) * a.kv_heads + kv) * P + id % P;
+      int8_t* const kdst = a.k + row * D + e0;
+      if constexpr (EPL == 8) *reinterpret_cast<uint2*>(kdst) = uint2{kw[0], kw[1]};
+      else *reinterpret_cast<uint32_t*>(kdst) = kw[0];
+      if (sub == 0) {
+        a.k_scales[row] = ks;
+        a.v_scales[row] = vs;
+      }
+    }
+  }
+  __syncthreads();
+  // V: item (d, group q) of D * 4, two per thread at D = 128.
+  for (uint32_t it = threadIdx.x; it < D * 4u; it += 64u * kWaves) {
+    const uint32_t d = it >> 2, q = it & 3u;
+    const uint8_t* const src = vt + d * 64u + 16u * q;
+    if (grp_ok[q]) {
+      const uint32_t id = ids[16u * q];
+      int8_t* const dst = a.v + (size_t(id / P) * a.kv_heads + kv) * D * P + size_t(d) * P + id % P;
+      *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
+    } else {
+#pragma unroll 4
+      for (uint32_t j = 0; j < 16u; ++j) {
+        const uint32_t id = ids[16u * q + j];
+        if (id < cap) a.v[(size_t(id / P) * a.kv_heads + kv) * D * P + size_t(d) * P + id % P] = int8_t(src[j]);
+      }
+    }
+  }
+}
+
 template <class T>
 hipError_t launch_typed(const AppendArgs& a, hipStream_t stream) {
   if (a.tokens < kTileMin) {
@@ -203,6 +309,21 @@ hipError_t launch_typed(const AppendArgs& a, hipStream_t stream) {
                    (uint64_t(a.k_stride) * es) % 16 == 0 && (uint64_t(a.v_stride) * es) % 16 == 0 &&
                    a.dim % (16u * kWaves) == 0 && reinterpret_cast<uintptr_t>(a.k) % 16 == 0;
   const dim3 grid((a.tokens + 63u) / 64u, a.kv_heads);
+  // Row-streaming kernel: 16-byte aligned sources and strides, aligned K and V
+  // pools, whole 16-slot groups in a page.
+  const bool stream_ok = vec && reinterpret_cast<uintptr_t>(a.v) % 16 == 0 && a.page_tokens % 16 == 0;
+  if (stream_ok && a.dim == 64) {
+    hipLaunchKernelGGL((append_stream_kernel<T, 64>), grid, dim3(64 * kWaves), 0, stream, a);
+    return hipGetLastError();
+  }
+  if (stream_ok && a.dim == 128) {
+    hipLaunchKernelGGL((append_stream_kernel<T, 128>), grid, dim3(64 * kWaves), 0, stream, a);
+    return hipGetLastError();
+  }
+  if (stream_ok && a.dim == 256) {
+    hipLaunchKernelGGL((append_stream_kernel<T, 256>), grid, dim3(64 * kWaves), 0, stream, a);
+    return hipGetLastError();
+  }
   if (vec) hipLaunchKernelGGL((append_tile_kernel<T, true>), grid, dim3(64 * kWaves), 0, stream, a);
   else hipLaunchKernelGGL((append_tile_kernel<T, false>), grid, dim3(64 * kWaves), 0, stream, a);
   return hipGetLastError();
@@ -229,7 +350,16 @@ hipError_t preload_append() {
                        reinterpret_cast<const void*>(&append_tile_kernel<_Float16, true>),
                        reinterpret_cast<const void*>(&append_tile_kernel<_Float16, false>),
                        reinterpret_cast<const void*>(&append_tile_kernel<__bf16, true>),
-                       reinterpret_cast<const void*>(&append_tile_kernel<__bf16, false>)};
+                       reinterpret_cast<const void*>(&append_tile_kernel<__bf16, false>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<float, 64>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<float, 128>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<float, 256>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<_Float16, 64>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<_Float16, 128>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<_Float16, 256>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<__bf16, 64>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<__bf16, 128>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<__bf16, 256>)};
   hipFuncAttributes attr{};
   for (const void* f : fns) {
     const hipError_t e = hipFuncGetAttributes(&attr, f);

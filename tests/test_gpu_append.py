@@ -43,13 +43,10 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("case", CASES)
-def test_append_matches_oracle_bitwise(gpu, case):
+def _run_append(gpu, tokens, kvh, D, P, src, extra, slots, pages, seed):
     import torch
 
-    tokens, kvh, D, P, src, extra = case
-    rng = np.random.default_rng(tokens * 31 + D)
-    pages = -(-tokens // P) + 3
+    rng = np.random.default_rng(seed)
     pool = random_pool(pages, kvh, P, D, seed=tokens)
     row = kvh * D
     stride = row + extra
@@ -59,9 +56,6 @@ def test_append_matches_oracle_bitwise(gpu, case):
     kbuf[0, :D] = 0                                   # an all-zero row
     vbuf[-1, :D] = torch.tensor(np.round(rng.standard_normal(D) * 4) / 2, dtype=tdt)  # exact halves
     vbuf[-1, 0] = 127
-    slots = rng.permutation(pages * P)[:tokens].astype(np.uint32)
-    if tokens > 3:
-        slots[2] = 0xFFFFFFFF                         # padding entry
     # host reference on the exactly representable fp32 values of the source
     kn = kbuf.float().numpy()[:, :row].reshape(tokens, kvh, D)
     vn = vbuf.float().numpy()[:, :row].reshape(tokens, kvh, D)
@@ -75,6 +69,42 @@ def test_append_matches_oracle_bitwise(gpu, case):
         got = g.cpu().numpy()
         assert np.array_equal(got.view(np.uint8) if got.dtype == np.int8 else got.view(np.uint32),
                               w.view(np.uint8) if w.dtype == np.int8 else w.view(np.uint32)), f"{name} differs"
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_append_matches_oracle_bitwise(gpu, case):
+    tokens, kvh, D, P, src, extra = case
+    rng = np.random.default_rng(tokens * 31 + D)
+    pages = -(-tokens // P) + 3
+    slots = rng.permutation(pages * P)[:tokens].astype(np.uint32)
+    if tokens > 3:
+        slots[2] = 0xFFFFFFFF                         # padding entry
+    _run_append(gpu, tokens, kvh, D, P, src, extra, slots, pages, seed=tokens * 31 + D)
+
+
+PREFILL_CASES = [
+    # tokens, kv_heads, dim, page, src, first slot offset in its page, padding entries
+    (4096, 8, 128, 64, kvb.KVB_SRC_F16, 0, ()),       # whole pages: every 16-slot group is one V store
+    (1000, 2, 256, 32, kvb.KVB_SRC_F32, 0, ()),       # ragged last tile and group
+    (700, 4, 64, 16, kvb.KVB_SRC_BF16, 8, ()),        # groups straddle 16-slot boundaries: byte stores
+    (520, 8, 128, 64, kvb.KVB_SRC_F16, 0, (100, 263)),  # padding inside two groups
+    (300, 1, 64, 64, kvb.KVB_SRC_F32, 48, ()),        # starts mid-page, crosses pages
+]
+
+
+@pytest.mark.parametrize("case", PREFILL_CASES)
+def test_append_prefill_mapping_matches_oracle_bitwise(gpu, case):
+    """A prefill chunk's slot mapping (consecutive slots of permuted pages),
+    the layout the row-streaming kernel stores 16 V codes at a time."""
+    tokens, kvh, D, P, src, off, pads = case
+    rng = np.random.default_rng(tokens * 7 + D)
+    pages = -(-(tokens + off) // P) + 2
+    order = rng.permutation(pages).astype(np.uint32)
+    t = np.arange(tokens, dtype=np.uint32) + off
+    slots = (order[t // P] * P + t % P).astype(np.uint32)
+    for i in pads:
+        slots[i] = 0xFFFFFFFF
+    _run_append(gpu, tokens, kvh, D, P, src, 0, slots, pages, seed=tokens * 7 + D)
 
 
 def test_cache_written_by_append_decodes(gpu):
