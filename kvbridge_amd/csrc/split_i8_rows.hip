@@ -4,12 +4,12 @@
 //
 // One work-group of four waves per (split, kv head) streams the split's KV
 // tiles through a two-slot LDS ring (CT tiles per slot: the tile images of
-// lds_stream.h) and every wave runs a
-// block of 16 head-rows over each tile, so the split's KV is read from HBM
-// once for all its head-rows.  While the waves compute phase p (slot p & 1),
-// the DMA of phase p + 1 is in flight; phase p + 2 is issued into the slot
-// after the barrier that ends phase p.  More than 64 head-rows (four
-// blocks) stream the split again per group of four blocks.
+// lds_stream.h), and wave w runs head-row block w (16 head-rows) over each
+// tile, so the split's KV is read from HBM once for all its head-rows.
+// While the waves compute phase p (slot p & 1), the DMA of phase p + 1 is in
+// flight; phase p + 2 is issued into the slot after the barrier that ends
+// phase p.  More than 64 head-rows (four blocks) stream the split again per
+// group of four blocks.
 //
 // Per phase, wave-local and exact in integers as in the single-block int8
 // kernel (split_i8.h):
@@ -19,11 +19,12 @@
 //  - phase maximum m_p per head-row, running maximum m = max(m, m_p); the
 //    fp32 numerators and denominators so far are rescaled by 2^(m_old - m).
 //  - PV: the weights 2^(s - m) * v_scale * 2^kp (below 2^20; kp from the
-//    phase's largest v-scale) as three 7-bit digits form B in the token order
-//    the QK result left in each lane (QK M-block mb takes tokens
+//    phase's largest v-scale) as three 7-bit digits form B in the token
+//    order the QK result left in each lane (QK M-block mb takes tokens
 //    16q + 4mb + r, so lane (h, g) holds tokens 16g .. 16g + 15, which are
-//    its k-positions of PV), so nothing moves between lanes.  Each 16-dim block's three int32
-//    digit sums over the phase are folded into fp32 at once (2^-kp).
+//    its k-positions of PV), so nothing moves between lanes.  Each 16-dim
+//    block's three int32 digit sums over the phase are folded into fp32 at
+//    once (2^-kp).
 // A wave owns whole head-rows and writes their partials from registers.
 // Requires splits that start on a 64-token tile (host-checked).
 #include <cstdio>
