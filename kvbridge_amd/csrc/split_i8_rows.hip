@@ -89,7 +89,7 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
     SplitArgs a, const float* __restrict__ q, const int64_t* __restrict__ qpos,
     const int64_t* __restrict__ kpos, const uint32_t* __restrict__ table,
     const int8_t* __restrict__ kdata, const int8_t* __restrict__ vdata,
-    const float* __restrict__ kscale, const float* __restrict__ vscale, float* __restrict__ scratch) {
+    const float* __restrict__ kscale, const float* __restrict__ vscale, float* __restrict__ scratch, uint32_t spw) {
   using G = Geo<D>;
   constexpr int CT = RowsGeo<D>::kCT;
   constexpr uint32_t kSlot = RowsGeo<D>::kSlot;
@@ -102,13 +102,21 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t n = lane & 15u, g = lane >> 4;
-  const uint32_t split = blockIdx.x, kv = blockIdx.y;
+  const uint32_t kv = blockIdx.y;
   const uint32_t head_rows = a.rows * a.group, hblocks = (head_rows + 15u) / 16u;
   const uint32_t rounds = (hblocks + kWaves - 1u) / kWaves;
 
-  const uint64_t s0_64 = uint64_t(a.begin) + uint64_t(split) * a.split_tokens;
+  // Splits [sp0, sp1) of this work-group, tokens [s0, s1).  With spw > 1 a
+  // split is a whole number of phases (pps; host-checked) and every split's
+  // partial is written at its last phase, so the partials are those of one
+  // work-group per split.
+  const uint32_t sp0 = blockIdx.x * spw;
+  const uint32_t sp1 = sp0 + spw < a.splits ? sp0 + spw : a.splits;
+  const uint32_t pps = a.split_tokens / (kTileTokens * CT);
+  const uint64_t s0_64 = uint64_t(a.begin) + uint64_t(sp0) * a.split_tokens;
   const uint32_t s0 = s0_64 < a.end ? uint32_t(s0_64) : a.end;
-  const uint32_t s1 = uint64_t(s0) + a.split_tokens < a.end ? s0 + a.split_tokens : a.end;
+  const uint64_t s1_64 = uint64_t(a.begin) + uint64_t(sp1) * a.split_tokens;
+  const uint32_t s1 = s1_64 < a.end ? uint32_t(s1_64) : a.end;
   const uint32_t k_first = s0 / kTileTokens;
   const uint32_t ntiles = s1 > s0 ? (s1 - 1u) / kTileTokens + 1u - k_first : 0u;
   const uint32_t nphase = (ntiles + CT - 1u) / CT;
@@ -274,6 +282,27 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
     f32x4 acc[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // This block's partial of split `split` from the registers (lane (h, g):
+    // dims 16mb + 4g + e), then a fresh state for the next split.
+    auto write_partial = [&](uint32_t split) __attribute__((always_inline)) {
+      if (!has) return;
+      const float l_h = rows_sum(l_run);
+      if (hvalid) {
+        float* const dst = scratch + ((size_t(row) * a.q_heads + head) * a.splits + split) * W;
+        if (g == 0) {
+          dst[0] = m_run * kLn2;
+          dst[1] = l_h;
+        }
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dst[2 + 16 * mb + 4 * g + e] = acc[mb][e];
+      }
+      m_run = neg_inf();
+      l_run = 0.f;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    };
 
     for (uint32_t p = 0; p < nphase; ++p) {
       if (issued(p + 1u)) wait_vm<G::kLoadsPerTile>();
@@ -427,35 +456,44 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
           }
         });
       }
+      if (p + 1u == nphase) write_partial(sp1 - 1u);
+      else if (spw > 1u && (p + 1u) % pps == 0u) write_partial(sp0 + p / pps);
       __syncthreads();  // slot p & 1 is free
       if (p + 2u < nphase) issue(p + 2u);
     }
-
-    // ---- this block's partials from the registers (lane (h, g): dims 16mb + 4g + e)
-    if (has) {
-      const float l_h = rows_sum(l_run);
-      if (hvalid) {
-        float* const dst = scratch + ((size_t(row) * a.q_heads + head) * a.splits + split) * W;
-        if (g == 0) {
-          dst[0] = m_run * kLn2;
-          dst[1] = l_h;
-        }
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) dst[2 + 16 * mb + 4 * g + e] = acc[mb][e];
-      }
+    if (nphase == 0) {  // empty range: empty partials
+      for (uint32_t sp = sp0; sp < sp1; ++sp) write_partial(sp);
     }
   }
 }
 
 #define KVB_I8R_ARGS                                                                             \
   a, a.q, a.q_positions, a.k_positions, a.page_table, static_cast<const int8_t*>(a.k),             \
-      static_cast<const int8_t*>(a.v), a.k_scales, a.v_scales, a.scratch
+      static_cast<const int8_t*>(a.v), a.k_scales, a.v_scales, a.scratch, spw
+
+// Compute units of the current device (cached per device).
+uint32_t device_cus() {
+  static uint32_t cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256u;
+  if (cache[dev] == 0u) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = uint32_t(n);
+  }
+  return cache[dev];
+}
 
 template <int D>
 hipError_t launch_dim(const SplitArgs& a, hipStream_t stream) {
-  const dim3 grid(a.splits, a.kv_heads);
+  // Short splits: several consecutive splits per work-group (one work-group
+  // per CU where there are enough), when a split is a whole number of phases.
+  uint32_t spw = 1u;
+  if ((a.split_tokens / kTileTokens) % RowsGeo<D>::kCT == 0u) {
+    const uint32_t per_cu = uint32_t((uint64_t(a.splits) * a.kv_heads) / device_cus());
+    spw = per_cu > 1u ? per_cu : 1u;
+  }
+  const dim3 grid((a.splits + spw - 1u) / spw, a.kv_heads);
   if (a.page_tokens % kTileTokens == 0)
     hipLaunchKernelGGL((split_i8_rows_kernel<D, true>), grid, dim3(64 * kWaves), 0, stream, KVB_I8R_ARGS);
   else

@@ -129,6 +129,9 @@ I8_ROWS_SHAPES = [
     (2, 48, 4, 128, 64, 1536, 64, 1500, 448, "causal", 0.05),  # 24 head-rows, 7-tile splits, ragged end
     (8, 96, 4, 128, 32, 3000, 0, 3000, 2048, "spread", 0.0),   # 192 head-rows: three streams of 4 blocks
     (8, 24, 4, 256, 32, 4096, 0, 4000, 1344, "causal", 0.0),   # dense geometry, 21-tile splits (odd phase)
+    # more (split, kv head) pairs than twice the CUs: several splits per work-group
+    (8, 24, 4, 256, 32, 32768, 0, 32768, 256, "causal", 0.0),  # 128 splits x 4 kv: two splits each
+    (4, 32, 8, 128, 64, 20000, 0, 19900, 256, "spread", 0.01),  # 78 splits x 8 kv, ragged last split
 ]
 
 
