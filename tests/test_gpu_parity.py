@@ -132,6 +132,7 @@ I8_ROWS_SHAPES = [
     # more (split, kv head) pairs than twice the CUs: several splits per work-group
     (8, 24, 4, 256, 32, 32768, 0, 32768, 256, "causal", 0.0),  # 128 splits x 4 kv: two splits each
     (4, 32, 8, 128, 64, 20000, 0, 19900, 256, "spread", 0.01),  # 78 splits x 8 kv, ragged last split
+    (8, 96, 4, 128, 64, 40000, 128, 40000, 256, "masked", 0.0),  # 192 head-rows (3 streams) x 2 splits each
 ]
 
 
