@@ -27,6 +27,7 @@
 //    once (2^-kp).
 // A wave owns whole head-rows and writes their partials from registers.
 // Requires splits that start on a 64-token tile (host-checked).
+#include <atomic>
 #include <cstdio>
 #include <type_traits>
 
@@ -471,17 +472,20 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
   a, a.q, a.q_positions, a.k_positions, a.page_table, static_cast<const int8_t*>(a.k),             \
       static_cast<const int8_t*>(a.v), a.k_scales, a.v_scales, a.scratch, spw
 
-// Compute units of the current device (cached per device).
+// Compute units of the current device (cached per device; callers on
+// several threads may fill an entry concurrently with the same value).
 uint32_t device_cus() {
-  static uint32_t cache[64] = {};
+  static std::atomic<uint32_t> cache[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256u;
-  if (cache[dev] == 0u) {
+  uint32_t v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0u) {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = uint32_t(n);
+    v = uint32_t(n);
+    cache[dev].store(v, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return v;
 }
 
 template <int D>
