@@ -993,9 +993,14 @@ hipError_t launch_dim(const SplitArgs& a, int cfg, hipStream_t stream) {
       if (cfg == 82) return launch_cfg<D, 8, 2, 4>(a, stream);
       if (cfg == 44) return launch_cfg<D, 4, 4, 4>(a, stream);
     }
+    if (cfg == 12) return launch_cfg<D, 1, 2, 4>(a, stream);
+    if (cfg == 14) return launch_cfg<D, 1, 4, 4>(a, stream);
     return cfg == 42 ? launch_cfg<D, 4, 2, 4>(a, stream) : launch_cfg<D, 2, 2, 4>(a, stream);
   }
-  if constexpr (D <= 128) return cfg == 42 ? launch_cfg<D, 4, 2, 8>(a, stream) : launch_cfg<D, 2, 2, 8>(a, stream);
+  if constexpr (D <= 128) {
+    if (cfg == 12) return launch_cfg<D, 1, 2, 8>(a, stream);
+    return cfg == 42 ? launch_cfg<D, 4, 2, 8>(a, stream) : launch_cfg<D, 2, 2, 8>(a, stream);
+  }
   return hipErrorInvalidValue;
 }
 
@@ -1010,6 +1015,11 @@ hipError_t preload_dim() {
   }
   if (e == hipSuccess) e = preload_cfg<D, 4, 2, 4>();
   if (e == hipSuccess) e = preload_cfg<D, 2, 2, 4>();
+  if (e == hipSuccess) e = preload_cfg<D, 1, 2, 4>();
+  if (e == hipSuccess) e = preload_cfg<D, 1, 4, 4>();
+  if constexpr (D <= 128) {
+    if (e == hipSuccess) e = preload_cfg<D, 1, 2, 8>();
+  }
   return e;
 }
 

@@ -28,7 +28,14 @@ constexpr uint32_t kTiles = 64;  // tokens per tile
 // head-rows, two waves for 8 head-rows (whose state takes one SIMD per
 // wave).  Measured on MI355X (configs[2] / configs[3] batched calls,
 // 2048-work-group grids): 118 / 216 us with these against 140 / 242 us with
-// the single-sequence choice.
+// the single-sequence choice.  Large grids of short splits (<= 32 tiles)
+// run one wave per work-group: the wave streams its split alone, so there is
+// no wave combine, no work-group barrier and no idle wave per split, and
+// eight such work-groups share a CU.  Measured: cfg2 through launch_attention
+// (its 256-token splits, 2,048 work-groups) 47.7 -> 25.3 us for the split
+// launch, configs[3] (64 chunks of 2,048 tokens, 8 head-rows) 203.5 -> 190.6
+// us; configs[2] at 5,120-token splits (80 tiles) stays on four waves (91
+// against 111 us).
 // KVB_I8_CFG="NW,NB" overrides (tuning sweeps; unknown pairs fall back).
 int i8_config(const SplitArgs& a) {
   static const int forced = [] {
@@ -39,9 +46,14 @@ int i8_config(const SplitArgs& a) {
   const uint32_t tiles = (a.split_tokens + kTiles - 1) / kTiles;
   const uint32_t hr = a.rows * a.group;
   const bool eight = hr <= 4 && a.dim <= 128;
-  if (forced == 42 || forced == 22 || ((forced == 82 || forced == 44) && eight)) return forced;
+  if (forced == 42 || forced == 22 || forced == 12 || ((forced == 82 || forced == 44) && eight) ||
+      (forced == 14 && hr <= 4))
+    return forced;
   const uint64_t groups = uint64_t(a.splits) * a.kv_heads * (a.seq_starts ? a.batch : 1u);
-  if (groups > 512u) return hr <= 4 && tiles >= 4 ? 42 : 22;
+  if (groups > 512u) {
+    if (tiles <= 32u) return 12;
+    return hr <= 4 ? 42 : 22;
+  }
   if (eight && tiles >= 16) return 82;
   return tiles >= 4 ? 42 : 22;
 }
