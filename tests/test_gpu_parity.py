@@ -172,6 +172,48 @@ def test_i8_rows_kernel_shapes(gpu, cfg):
         assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
 
 
+SCALE_SHAPES = [
+    # rows, q_heads, kv_heads, dim, P, tokens, split_tokens, kernel family
+    (1, 8, 2, 128, 64, 2048, 512, "split_i8_kernel<"),
+    (8, 24, 4, 256, 32, 2048, 256, "split_i8_rows_kernel<"),
+    (4, 24, 4, 64, 16, 1000, 256, "split_lds_rows_kernel<"),
+]
+
+
+@pytest.mark.parametrize("score_scale", [-0.0883883, 0.0, 0.75])
+@pytest.mark.parametrize("cfg", SCALE_SHAPES)
+def test_score_scale_sign_and_zero(gpu, cfg, score_scale):
+    """The shape contract accepts any finite score scale: negative scales
+    reverse the score order, and a zero scale makes every visible token's
+    weight equal (the output is the plain mean of the visible V rows)."""
+    rows, qh, kvh, d, p, t, st, family = cfg
+    seed = zlib.crc32(repr((cfg, score_scale)).encode()) & 0xFFFF
+    qpos = _query_positions("spread", rows, 0, t, np.random.default_rng(seed))
+    case = W.synth_case(rows, qh, kvh, d, p, t, seed=seed, qpos=qpos, scale=score_scale)
+    name = kvb.selected_kernel_name(case.shape, kvb.device_input(*([0x1000] * 8)), st)
+    log(f"scale={score_scale} shape={case.shape.as_tuple()} split_tokens={st} kernel={name}")
+    assert name.startswith(family), name
+    dc = DeviceCase(case)
+    ref = O.fp64(case, threads=8)
+    mln, _, _ = dc.run_decode(st)
+    check_against_oracle(case, mln, f"decode scale={score_scale}", ref)
+    if score_scale == 0.0:  # closed form: the mean of the visible dequantised V rows
+        _, l, n = (np.asarray(x, dtype=np.float64) for x in mln)
+        l, n = l.reshape(-1), n.reshape(rows * qh, d)
+        tok = np.arange(t)
+        page, slot = case.table[tok // p].astype(np.int64), tok % p
+        for r in range(rows):
+            vis = case.kpos <= case.qpos[r]
+            if not vis.any():  # row 0 sees nothing: the empty convention
+                assert np.all(l[r * qh:(r + 1) * qh] == 0) and np.all(n[r * qh:(r + 1) * qh] == 0)
+                continue
+            out = n / np.where(l > 0, l, 1)[:, None]
+            for h in (0, qh - 1):
+                kv = h // (qh // kvh)
+                vrows = case.v[page, kv, :, slot].astype(np.float64) * case.vs[page, kv, slot][:, None]
+                np.testing.assert_allclose(out[r * qh + h], vrows[vis].mean(axis=0), rtol=0, atol=2e-3)
+
+
 GENERIC_SHAPES = [
     # rows, q_heads, kv_heads, dim, P, tokens, begin, end, split_tokens, int8
     (1, 8, 2, 100, 16, 600, 0, 600, 256, True),
