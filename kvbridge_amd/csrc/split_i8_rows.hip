@@ -263,7 +263,8 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
         for (int i = 0; i < 4; ++i) w[0][i] = w[1][i] = w[2][i] = 0u;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int qi = int(__builtin_rintf(__builtin_amdgcn_ldexpf(qv[s][i], kq)));  // |qi| <= 2^21
+          int qi = int(__builtin_rintf(__builtin_amdgcn_ldexpf(qv[s][i], kq)));  // |qi| <= 2^21
+          if (a.scale < 0.f) qi = -qi;  // scores scale by |scale| (see cs)
           const int lo8 = __builtin_amdgcn_sbfe(qi, 0, 8);
           const int r1 = (qi - lo8) >> 8;
           const int mid8 = __builtin_amdgcn_sbfe(r1, 0, 8);
@@ -275,7 +276,12 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
 #pragma unroll
         for (int dg = 0; dg < 3; ++dg) qd[dg][s] = i32x4{int(w[dg][0]), int(w[dg][1]), int(w[dg][2]), int(w[dg][3])};
       }
-      cs = __builtin_amdgcn_ldexpf(a.scale, -kq) * kLog2e;  // score factor, log2 units
+      // Score factor in log2 units, > 0: the sign of the scale went into the
+      // Q digits, and a zero factor becomes the smallest normal float (every
+      // score then rounds to 0 in 2^(cs * y - mu) while masked y = -inf
+      // stays -inf instead of 0 * inf).
+      cs = __builtin_amdgcn_ldexpf(fabsf(a.scale), -kq) * kLog2e;
+      cs = cs >= 1.17549435e-38f ? cs : 1.17549435e-38f;
     }
     const uint32_t nvis = has && e_max > s0 ? (e_max - 1u) / kTileTokens + 1u - k_first : 0u;  // tiles
 
@@ -318,7 +324,9 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
         for (int s = 0; s < KS; ++s) ka[s] = pb + koff[s];
         const uint32_t va = pb + voff, sa = pb + soff, vma = pb + vmoff;
 
-        // ---- QK: scores of the phase's tiles, lane (h, g): tokens 16g + 4mb + e
+        // ---- QK: scores of the phase's tiles, lane (h, g): tokens 16g + 4mb + e,
+        // as y = (integer dot) * k_scale; the score in log2 units is cs * y
+        // (cs > 0, so maxima of y are maxima of scores).
         float sc[CT][16];
         float mx = neg_inf();
         static_for<0, CT>([&](auto jc) __attribute__((always_inline)) {
@@ -357,7 +365,7 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 const int hi2 = cq[0][mb][e] * 256 + cq[1][mb][e];  // |.| < 2^29
-                float s2 = fmaf(float(hi2), 256.f, float(cq[2][mb][e])) * (__uint_as_float(ks[mb][e]) * cs);
+                float s2 = fmaf(float(hi2), 256.f, float(cq[2][mb][e])) * __uint_as_float(ks[mb][e]);
                 if constexpr (MASK) s2 = 16u * g + 4u * mb + e < vis ? s2 : neg_inf();
                 sc[j][4 * mb + e] = s2;
                 mx = fmaxf(mx, s2);
@@ -380,7 +388,7 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
           const uint32_t t0 = (k_first + tp + j) * kTileTokens;
           vm = t0 + lane < e_max ? fmaxf(vm, fabsf(v)) : vm;
         });
-        const float m_new = fmaxf(m_run, rows_max(mx));
+        const float m_new = fmaxf(m_run, rows_max(mx) * cs);
         const float vmax = wave_max(vm);
         int kp = 0;
         if (vmax > 0.f) {
@@ -412,14 +420,18 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
               bw[0][mb] = bw[1][mb] = bw[2][mb] = 0u;
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
-                const float w = __builtin_amdgcn_exp2f(sc[j][4 * mb + e] - mu);  // w * 2^kp
+                const float w = __builtin_amdgcn_exp2f(fmaf(sc[j][4 * mb + e], cs, -mu));  // w * 2^kp
                 lw += w;
                 float vsl = __uint_as_float(vsr[j][mb][e]);
                 if constexpr (MASK) vsl = 16u * g + 4u * mb + e < vlim ? vsl : 0.f;  // slots past the data
-                const int pint = int(__builtin_rintf(w * vsl));
-                bw[0][mb] |= (uint32_t(pint >> 14) & 0xffu) << (8 * e);
-                bw[1][mb] |= ((uint32_t(pint) >> 7) & 0x7fu) << (8 * e);
-                bw[2][mb] |= (uint32_t(pint) & 0x7fu) << (8 * e);
+                // p = w * v_scale rounded to an integer (|p| < 2^20) in one fma:
+                // 1.5 * 2^23 + p lies in [2^23, 2^24), where the float's ulp is
+                // 1, so its low 22 bits are p mod 2^22 (two's complement), and
+                // bits 0-6, 7-13 and 14-21 are the three digits of p.
+                const uint32_t pb = __float_as_uint(fmaf(w, vsl, 12582912.f));
+                bw[0][mb] |= ((pb >> 14) & 0xffu) << (8 * e);
+                bw[1][mb] |= ((pb >> 7) & 0x7fu) << (8 * e);
+                bw[2][mb] |= (pb & 0x7fu) << (8 * e);
               }
             }
           };
