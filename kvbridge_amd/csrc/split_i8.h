@@ -748,10 +748,14 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
       constexpr uint32_t h = decltype(hc)::value;
       const float w = __builtin_amdgcn_exp2f(sc[r][h] - mu[h]);  // w * 2^kp
       lw[h] += w;
-      const int pint = int(__builtin_rintf(w * vs_l));
-      const uint32_t d0 = uint32_t(pint >> 14) & 0xffu;
-      const uint32_t d1 = (uint32_t(pint) >> 7) & 0x7fu;
-      const uint32_t d2 = uint32_t(pint) & 0x7fu;
+      // p = w * v_scale rounded to an integer (|p| < 2^20) in one fma:
+      // 1.5 * 2^23 + p lies in [2^23, 2^24), where the float's ulp is 1, so
+      // its low 22 bits are p mod 2^22 (two's complement), and bits 0-6,
+      // 7-13 and 14-21 are the three digits of p.
+      const uint32_t pb = __float_as_uint(fmaf(w, vs_l, 12582912.f));
+      const uint32_t d0 = (pb >> 14) & 0xffu;
+      const uint32_t d1 = (pb >> 7) & 0x7fu;
+      const uint32_t d2 = pb & 0x7fu;
       dig_w[h * L::kDigCol] = uint8_t(d0);
       dig_w[(HS + h) * L::kDigCol] = uint8_t(d1);
       dig_w[(2 * HS + h) * L::kDigCol] = uint8_t(d2);
