@@ -177,6 +177,11 @@ def hbm_read_probe(src, nbytes: int, sink, blocks: int, stream=None) -> None:
     check(load().kvb_hbm_read_probe(_ptr(src), nbytes, _ptr(sink), blocks, _stream(stream)))
 
 
+def paged_read_probe(s: Shape, inp: DeviceInput, split_tokens: int, sink, stream=None) -> None:
+    """Diagnostic read of a decode call's KV bytes through its page table (see kvb_paged_read_probe)."""
+    check(load().kvb_paged_read_probe(ctypes.byref(s), ctypes.byref(inp), split_tokens, _ptr(sink), _stream(stream)))
+
+
 # ---- batched ragged decode (kvb_decode_attention_batched) ---------------------
 
 def make_batch_shape(batch, rows, q_heads, kv_heads, dim, page_tokens, pages, max_tokens, total_tokens,

@@ -142,6 +142,7 @@ SIGNATURES = [
     ("kvb_selected_kernel", _INT, [_SP, _IP, _U32]),
     ("kvb_selected_kernel_name", ctypes.c_char_p, [_SP, _IP, _U32, _INT]),
     ("kvb_hbm_read_probe", _INT, [_VP, ctypes.c_size_t, _VP, _U32, _VP]),
+    ("kvb_paged_read_probe", _INT, [_SP, _IP, _U32, _VP, _VP]),
     ("kvb_batch_shape_error", ctypes.c_char_p, [_BSP]),
     ("kvb_batch_split_count", _INT, [_BSP, ctypes.POINTER(_U32)]),
     ("kvb_batch_scratch_elements", _INT, [_BSP, ctypes.POINTER(ctypes.c_size_t)]),

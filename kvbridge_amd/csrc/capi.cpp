@@ -297,9 +297,14 @@ int kvb_launch_attention(const kvb_shape* sp, const kvb_device_input* ip, float*
     if (const char* e = launch_error(s, in, scratch)) return fail(KVB_EINVAL, e);
     const unsigned splits = kvbridge::split_count(s);
     const auto st = static_cast<hipStream_t>(stream);
-    int rc = run_split(s, in, kvbridge::kSplitTokens, splits, scratch, st, "split launch");
+    // Launch-failure messages name the reference's launches
+    // (src/attention_shared.cu:354-365): its shared-group kernel serves
+    // group <= 8, its legacy per-head kernel larger groups.
+    const bool legacy = s.q_heads / s.kv_heads > 8u;
+    int rc = run_split(s, in, kvbridge::kSplitTokens, splits, scratch, st,
+                       legacy ? "reference legacy split launch" : "reference split launch");
     if (rc != KVB_OK) return rc;
-    return run_merge(s, scratch, splits, m, l, n, nullptr, KVB_OUT_NONE, st, "merge launch");
+    return run_merge(s, scratch, splits, m, l, n, nullptr, KVB_OUT_NONE, st, "reference merge launch");
   });
 }
 
@@ -314,6 +319,10 @@ int kvb_launch_attention_mma(const kvb_shape* sp, const kvb_device_input* ip, fl
     if (!kvbridge::attention_mma_supported(s))
       return fail(KVB_EINVAL,
                   "launch_attention_mma requires int8 KV, rows8/group6/dim256/page32 and a page-aligned begin");
+    // Current-device check before the launch (src/attention_mma.cu:39).
+    int device = 0;
+    if (const int rc = hip_status(hipGetDevice(&device), "MMA current-context preparation"); rc != KVB_OK)
+      return rc;
     // The geometry always qualifies for the tiled MFMA kernel; buffers that
     // are 4- but not 16-byte aligned take the generic kernel (same results).
     const unsigned splits = kvbridge::split_count(s);
@@ -437,6 +446,27 @@ int kvb_hbm_read_probe(const void* src, size_t bytes, uint32_t* sink, uint32_t b
     return fail(KVB_EINVAL, "probe needs non-null 16-byte-multiple source, a sink and blocks > 0");
   return hip_status(kvb::launch_read_probe(src, bytes, sink, blocks, static_cast<hipStream_t>(stream)),
                     "read probe launch");
+}
+
+int kvb_paged_read_probe(const kvb_shape* sp, const kvb_device_input* ip, uint32_t split_tokens, uint32_t* sink,
+                         void* stream) {
+  return guarded([&]() -> int {
+    if (!sp || !ip || !sink) return fail(KVB_EINVAL, "shape, input and sink must be non-null");
+    const kvbridge::Shape s = to_shape(*sp);
+    const kvbridge::DeviceInput in = to_input(*ip);
+    if (const char* e = launch_error(s, in, sink)) return fail(KVB_EINVAL, e);
+    const auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (!s.int8 || (s.dim != 64 && s.dim != 128 && s.dim != 256) || s.page_tokens % 64 != 0 || split_tokens % 64 != 0 ||
+        s.begin % 64 != 0 || !al16(in.k) || !al16(in.v))
+      return fail(KVB_EINVAL,
+                  "paged probe needs int8 KV, dim 64/128/256, 64-token-aligned pages, splits and begin, "
+                  "16-byte aligned K/V");
+    const unsigned splits = kvbridge::split_count(s, split_tokens);
+    return hip_status(kvb::launch_paged_read_probe(in.page_table, in.k, in.v, in.k_scales, in.v_scales, s.kv_heads,
+                                                   s.dim, s.page_tokens, s.pages, s.begin, s.end, split_tokens,
+                                                   splits, sink, static_cast<hipStream_t>(stream)),
+                      "paged read probe launch");
+  });
 }
 
 int kvb_selected_kernel(const kvb_shape* sp, const kvb_device_input* ip, uint32_t split_tokens) {

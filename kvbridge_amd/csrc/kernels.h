@@ -99,6 +99,13 @@ hipError_t preload_append();
 // Streaming HBM read probe (diagnostic).
 hipError_t launch_read_probe(const void* src, size_t bytes, uint32_t* sink, uint32_t blocks,
                              hipStream_t stream);
+// Paged read probe (diagnostic): a decode call's K, V and scale bytes read
+// through its page table, no arithmetic (dim 64/128/256, page_tokens a
+// multiple of 64, 16-byte aligned K and V).
+hipError_t launch_paged_read_probe(const uint32_t* table, const void* k, const void* v, const float* ks,
+                                   const float* vs, uint32_t kv_heads, uint32_t dim, uint32_t page_tokens,
+                                   uint32_t pages, uint32_t begin, uint32_t end, uint32_t split_tokens,
+                                   uint32_t splits, uint32_t* sink, hipStream_t stream);
 
 hipError_t preload_lds();
 hipError_t preload_i8();

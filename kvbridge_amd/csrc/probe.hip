@@ -6,6 +6,9 @@
 // run of 8 KiB items, each wave reads whole items (64 lanes x 8 x 16-byte
 // non-temporal loads, one item in flight).  It plays the role of the
 // reference's same-layout stream probe (data/att-bench-65536-v2-07.json:528-541).
+// paged_read_probe_kernel reads a decode call's KV bytes through its page
+// table (random 8 KiB items) with the decode kernel's work split: the read
+// floor of the decode access pattern.
 #include "kernels.h"
 #include "device_common.h"
 
@@ -42,7 +45,76 @@ __global__ __launch_bounds__(kThreads) void read_probe_kernel(const u32x4* __res
   if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
 }
 
+// Same bytes and access pattern as a decode call through the page table,
+// with no arithmetic: work-group (split, kv head) of 8 waves, wave w taking
+// 64-token tiles w, w + 8, ... of its split; per tile the K rows (64 x dim
+// contiguous bytes), the V rows (dim rows of 64 bytes, stride page_tokens)
+// and the 64 k- and v-scales are requested together, one tile in flight per
+// wave.  Tiles lie in one page (page_tokens a multiple of 64).
+template <int D>
+__global__ __launch_bounds__(kThreads) void paged_read_probe_kernel(
+    const uint32_t* __restrict__ table, const int8_t* __restrict__ k, const int8_t* __restrict__ v,
+    const uint32_t* __restrict__ ks, const uint32_t* __restrict__ vs, uint32_t kv_heads, uint32_t page_tokens,
+    uint32_t pages, uint32_t begin, uint32_t end, uint32_t split_tokens, uint32_t* __restrict__ sink) {
+  constexpr uint32_t kPieces = D / 16;  // 16-byte pieces per lane and tile, for K and for V
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t split = blockIdx.x, kv = blockIdx.y;
+  const uint32_t s0 = begin + split * split_tokens;
+  const uint32_t s1 = s0 + split_tokens < end ? s0 + split_tokens : end;
+  uint32_t acc = 0;
+  for (uint32_t t0 = s0 + 64u * wave; t0 < s1; t0 += 64u * kWaves) {
+    uint32_t page = table[t0 / page_tokens];
+    page = page < pages ? page : pages - 1u;
+    const size_t slab = size_t(page) * kv_heads + kv;
+    const uint32_t slot0 = t0 % page_tokens;
+    const u32x4* kp = reinterpret_cast<const u32x4*>(k + (slab * page_tokens + slot0) * D);
+    u32x4 kx[kPieces], vx[kPieces];
+#pragma unroll
+    for (uint32_t j = 0; j < kPieces; ++j) kx[j] = __builtin_nontemporal_load(kp + 64u * j + lane);
+#pragma unroll
+    for (uint32_t j = 0; j < kPieces; ++j) {
+      const uint32_t piece = 64u * j + lane, row = piece >> 2, seg = piece & 3u;
+      vx[j] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(v + (slab * D + row) * page_tokens + slot0 + 16u * seg));
+    }
+    const uint32_t a = __builtin_nontemporal_load(ks + slab * page_tokens + slot0 + lane);
+    const uint32_t b = __builtin_nontemporal_load(vs + slab * page_tokens + slot0 + lane);
+    acc ^= a ^ b;
+#pragma unroll
+    for (uint32_t j = 0; j < kPieces; ++j) acc ^= kx[j][0] ^ kx[j][1] ^ kx[j][2] ^ kx[j][3] ^ vx[j][0] ^ vx[j][1] ^ vx[j][2] ^ vx[j][3];
+  }
+  if (acc == 0x9e3779b9u) sink[blockIdx.y * gridDim.x + blockIdx.x] = acc;
+}
+
 }  // namespace
+
+hipError_t launch_paged_read_probe(const uint32_t* table, const void* k, const void* v, const float* ks,
+                                   const float* vs, uint32_t kv_heads, uint32_t dim, uint32_t page_tokens,
+                                   uint32_t pages, uint32_t begin, uint32_t end, uint32_t split_tokens,
+                                   uint32_t splits, uint32_t* sink, hipStream_t stream) {
+  const dim3 grid(splits, kv_heads);
+  const auto* k8 = static_cast<const int8_t*>(k);
+  const auto* v8 = static_cast<const int8_t*>(v);
+  const auto* ks32 = reinterpret_cast<const uint32_t*>(ks);
+  const auto* vs32 = reinterpret_cast<const uint32_t*>(vs);
+  switch (dim) {
+    case 64:
+      hipLaunchKernelGGL(paged_read_probe_kernel<64>, grid, dim3(kThreads), 0, stream, table, k8, v8, ks32, vs32,
+                         kv_heads, page_tokens, pages, begin, end, split_tokens, sink);
+      break;
+    case 128:
+      hipLaunchKernelGGL(paged_read_probe_kernel<128>, grid, dim3(kThreads), 0, stream, table, k8, v8, ks32, vs32,
+                         kv_heads, page_tokens, pages, begin, end, split_tokens, sink);
+      break;
+    case 256:
+      hipLaunchKernelGGL(paged_read_probe_kernel<256>, grid, dim3(kThreads), 0, stream, table, k8, v8, ks32, vs32,
+                         kv_heads, page_tokens, pages, begin, end, split_tokens, sink);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_read_probe(const void* src, size_t bytes, uint32_t* sink, uint32_t blocks,
                              hipStream_t stream) {

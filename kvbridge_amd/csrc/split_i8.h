@@ -238,53 +238,47 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
   auto row_head = [&](uint32_t hh) __attribute__((always_inline)) {
     return size_t(hh / a.group) * a.q_heads + kv * a.group + hh % a.group;
   };
-  // Common case (<= 32 splits, one output per thread, one head-row per
-  // wave): straight-line code that requests every operand at once -- the
-  // wave's (m_j, l_j) and the thread's 32 numerators, split indices clamped
-  // instead of branched on -- so the merge costs one memory round trip.
-  if (ns <= kCh && outs <= 64u * NW && head_rows <= uint32_t(NW)) {
+  // Common case (<= 32 splits, one output per thread): straight-line code
+  // that requests every operand at once -- the wave's (m_j, l_j) and the
+  // thread's 32 numerators, split indices clamped instead of branched on --
+  // so the merge costs one memory round trip.  The 64 outputs of a wave lie
+  // in one head-row (64 divides D), so every wave turns its own head-row's
+  // (m_j, l_j) into the factors e^{m_j - M} (lane j holds split j) and reads
+  // them back with readlane: no LDS exchange and no work-group barrier.
+  if (ns <= kCh && outs <= 64u * NW) {
+    static_assert(D % 64 == 0, "a wave's outputs lie in one head-row");
+    if (64u * wave >= outs) return;
     const uint32_t jmax = ns - 1u;
-    const bool fw = wave < head_rows;
-    const float* fb = scratch + row_head(fw ? wave : 0u) * a.splits * W;
+    const uint32_t hh = (64u * wave) / D;
+    const float* fb = scratch + row_head(hh) * a.splits * W;
     const uint32_t jl = lane < ns ? lane : jmax;
     const float mj = ld_agent(fb + size_t(jl) * W);
     const float lj = ld_agent(fb + size_t(jl) * W + 1);
-    const bool ot = tid < outs;
-    const uint32_t o = ot ? tid : 0u;
-    const float* nb = scratch + row_head(o / D) * a.splits * W + 2 + o % D;
+    const uint32_t d = tid % D;
+    const float* nb = fb + 2 + d;
     float pre[kCh];
 #pragma unroll
     for (uint32_t j = 0; j < kCh; ++j) pre[j] = ld_agent(nb + size_t(j < jmax ? j : jmax) * W);
-    if (fw) {
-      const bool in = lane < ns;
-      const float mx = wave_max(in ? mj : neg_inf());
-      const float f = in && lj > 0.f ? exp_e(mj - mx) : 0.f;
-      const float lsum = wave_sum(f * lj);
-      if (lane < kCh) f_s[wave * kCh + lane] = f;
-      if (lane == 0) {
-        ml_s[2 * wave] = mx;
-        ml_s[2 * wave + 1] = lsum;
-      }
-    }
-    __syncthreads();
-    if (ot) {
-      const uint32_t hh = o / D, d = o % D;
-      const float* fh = f_s + hh * kCh;
-      float nacc = 0.f;
+    const bool in = lane < ns;
+    const float mx = wave_max(in ? mj : neg_inf());
+    const float f = in && lj > 0.f ? exp_e(mj - mx) : 0.f;
+    const float lsum = wave_sum(f * lj);
+    float nacc = 0.f;
 #pragma unroll
-      for (uint32_t j = 0; j < kCh; ++j) nacc = fmaf(fh[j], j <= jmax ? pre[j] : 0.f, nacc);
-      const size_t rh = row_head(hh);
-      const float lsum = ml_s[2 * hh + 1];
-      if (d == 0) {
-        a.m[rh] = ml_s[2 * hh];
-        a.l[rh] = lsum;
-      }
-      a.n[rh * D + d] = nacc;
-      if (a.out_type != 0) {
-        const float ov = lsum > 0.f ? nacc / lsum : 0.f;
-        if (a.out_type == 1) static_cast<float*>(a.out)[rh * D + d] = ov;
-        else static_cast<_Float16*>(a.out)[rh * D + d] = (_Float16)ov;
-      }
+    for (uint32_t j = 0; j < kCh; ++j) {
+      const float fj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), int(j)));
+      nacc = fmaf(fj, j <= jmax ? pre[j] : 0.f, nacc);
+    }
+    const size_t rh = row_head(hh);
+    if (d == 0) {
+      a.m[rh] = mx;
+      a.l[rh] = lsum;
+    }
+    a.n[rh * D + d] = nacc;
+    if (a.out_type != 0) {
+      const float ov = lsum > 0.f ? nacc / lsum : 0.f;
+      if (a.out_type == 1) static_cast<float*>(a.out)[rh * D + d] = ov;
+      else static_cast<_Float16*>(a.out)[rh * D + d] = (_Float16)ov;
     }
     return;
   }
@@ -379,13 +373,25 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
 }
 
 // VARLEN: batched call, grid.z = sequence (arguments rebased per work-group).
+// The leading scalar arguments are everything the first KV request depends
+// on; the translation units that instantiate this kernel are built with
+// kernel-argument preloading for them (the dispatcher places them in SGPRs),
+// so the page-table load is issued without waiting for a kernel-argument
+// load.  They duplicate fields of a_in, which the kernel overrides with them.
 template <int D, int NW, int NB, bool PT, int HS, bool FUSED, bool VARLEN>
 __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
-    SplitArgs a_in, const float* __restrict__ q_in, const int64_t* __restrict__ qpos_in,
-    const int64_t* __restrict__ kpos_in, const uint32_t* __restrict__ table_in,
-    const int8_t* __restrict__ kdata, const int8_t* __restrict__ vdata,
-    const float* __restrict__ kscale, const float* __restrict__ vscale, float* __restrict__ scratch_in) {
+    const uint32_t* __restrict__ table_in, const int8_t* __restrict__ kdata, const float* __restrict__ kscale,
+    const float* __restrict__ vscale, uint32_t p_begin, uint32_t p_end, uint32_t p_split_tokens,
+    uint32_t p_page_tokens, uint32_t p_kv_heads, uint32_t p_pages, SplitArgs a_in,
+    const float* __restrict__ q_in, const int64_t* __restrict__ qpos_in, const int64_t* __restrict__ kpos_in,
+    const int8_t* __restrict__ vdata, float* __restrict__ scratch_in) {
   SplitArgs a = a_in;
+  a.begin = p_begin;
+  a.end = p_end;
+  a.split_tokens = p_split_tokens;
+  a.page_tokens = p_page_tokens;
+  a.kv_heads = p_kv_heads;
+  a.pages = p_pages;
   if constexpr (VARLEN) rebase_sequence(a, blockIdx.z);
   const float* __restrict__ q = VARLEN ? a.q : q_in;
   const int64_t* __restrict__ qpos = VARLEN ? a.q_positions : qpos_in;
@@ -947,9 +953,10 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
   }
 }
 
-#define KVB_I8_ARGS                                                                              \
-  a, a.q, a.q_positions, a.k_positions, a.page_table, static_cast<const int8_t*>(a.k),             \
-      static_cast<const int8_t*>(a.v), a.k_scales, a.v_scales, a.scratch
+#define KVB_I8_ARGS                                                                                        \
+  a.page_table, static_cast<const int8_t*>(a.k), a.k_scales, a.v_scales, a.begin, a.end, a.split_tokens,     \
+      a.page_tokens, a.kv_heads, a.pages, a, a.q, a.q_positions, a.k_positions, static_cast<const int8_t*>(a.v), \
+      a.scratch
 
 template <int D, int NW, int NB, int HS>
 hipError_t launch_cfg(const SplitArgs& a, hipStream_t stream) {

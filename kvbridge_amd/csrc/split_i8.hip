@@ -40,8 +40,10 @@ constexpr uint32_t kTiles = 64;  // tokens per tile
 int i8_config(const SplitArgs& a) {
   static const int forced = [] {
     const char* e = std::getenv("KVB_I8_CFG");
-    if (!e) return 0;
-    return std::atoi(e) * 10 + std::atoi(e + 2);
+    int nw = 0, nb = 0;
+    char tail = 0;
+    if (!e || std::sscanf(e, "%d,%d%c", &nw, &nb, &tail) != 2 || nw < 1 || nw > 9 || nb < 1 || nb > 9) return 0;
+    return nw * 10 + nb;
   }();
   const uint32_t tiles = (a.split_tokens + kTiles - 1) / kTiles;
   const uint32_t hr = a.rows * a.group;
