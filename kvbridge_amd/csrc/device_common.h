@@ -13,6 +13,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// PV weight scaling of the int8-digit kernels: p = round(w * v_scale * 2^kp)
+// with kp = 21 - exponent(v_max * kVmaxMargin) stays below 2^21 - 1 (w <= 1),
+// so its top 7-bit digit is at most 127.  Without the margin a v_max just
+// below a power of two could round p up to 2^21.
+constexpr float kVmaxMargin = 1.0f + 1.0f / 1048576.0f;  // 1 + 2^-20
+
 // e^x as 2^(x * log2 e) on the hardware base-2 exponential (v_exp_f32).
 // exp(-inf) = 0.  Callers never pass NaN-producing (-inf) - (-inf).
 __device__ __forceinline__ float exp_e(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }

@@ -3,12 +3,12 @@
 //
 // The INT8 codes are never converted: both contractions run on
 // v_mfma_i32_16x16x64_i8 with the raw K and V bytes as the A operand.
-//  * QK: Q of each head-row is scaled by a power of two to a 22-bit integer
+//  * QK: Q of each head-row is scaled by a power of two to a 23-bit integer
 //    and split into three int8 digits (q = hi*2^16 + mid*2^8 + lo, exact).
 //    The digits of all head-rows sit side by side in the 16 MFMA columns
 //    (column = digit * HS + head), so one MFMA per 64 dims gives all three
 //    digit dot products for 16 tokens.
-//  * PV: the weights w * v_scale are scaled by 2^kp to integers below 2^20
+//  * PV: the weights w * v_scale are scaled by 2^kp to integers below 2^21
 //    and split into three 7-bit digits (p = d0*2^14 + d1*2^7 + d2); the
 //    per-digit integer numerators accumulate exactly in int32.
 // Digit recombination and the softmax run in a transposed view where each
@@ -581,7 +581,7 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
       amax = rows_max(amax);
       int kq = 0;
       if (amax > 0.f) {
-        kq = 21 - __builtin_amdgcn_frexp_expf(amax);
+        kq = 22 - __builtin_amdgcn_frexp_expf(amax);  // |2^kq q| < 2^22: top digit in [-64, 64]
         kq = kq < -100 ? -100 : (kq > 100 ? 100 : kq);
       }
       return kq;
@@ -754,7 +754,7 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
       constexpr uint32_t h = decltype(hc)::value;
       const float w = __builtin_amdgcn_exp2f(sc[r][h] - mu[h]);  // w * 2^kp
       lw[h] += w;
-      // p = w * v_scale rounded to an integer (|p| < 2^20) in one fma:
+      // p = w * v_scale rounded to an integer (0 <= p < 2^21) in one fma:
       // 1.5 * 2^23 + p lies in [2^23, 2^24), where the float's ulp is 1, so
       // its low 22 bits are p mod 2^22 (two's complement), and bits 0-6,
       // 7-13 and 14-21 are the three digits of p.
@@ -795,7 +795,7 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
     vmx = 0.f;
     kp = 0;
     if (vmax > 0.f) {
-      kp = 20 - __builtin_amdgcn_frexp_expf(vmax);
+      kp = 21 - __builtin_amdgcn_frexp_expf(vmax * kVmaxMargin);
       kp = kp < -100 ? -100 : (kp > 100 ? 100 : kp);
     }
 #pragma unroll

@@ -14,11 +14,11 @@
 // Per phase, wave-local and exact in integers as in the single-block int8
 // kernel (split_i8.h):
 //  - QK: v_mfma_i32_16x16x64_i8 with the raw INT8 K codes as A and digit dg
-//    (hi, mid, lo) of the 22-bit integer 2^kq * q of the block's 16 head-rows
+//    (hi, mid, lo) of the 23-bit integer 2^kq * q of the block's 16 head-rows
 //    as B; the three digit products of a (token, head-row) land in one lane.
 //  - phase maximum m_p per head-row, running maximum m = max(m, m_p); the
 //    fp32 numerators and denominators so far are rescaled by 2^(m_old - m).
-//  - PV: the weights 2^(s - m) * v_scale * 2^kp (below 2^20; kp from the
+//  - PV: the weights 2^(s - m) * v_scale * 2^kp (below 2^21; kp from the
 //    phase's largest v-scale) as three 7-bit digits form B in the token
 //    order the QK result left in each lane (QK M-block mb takes tokens
 //    16q + 4mb + r, so lane (h, g) holds tokens 16g .. 16g + 15, which are
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
       e_max = __builtin_amdgcn_readfirstlane(hi);
 
       // Q digits (B of QK): lane (h, g) holds dims 64s + 16g .. +15 of
-      // head-row h; digit dg of the 22-bit integer 2^kq * q in qd[dg].
+      // head-row h; digit dg of the 23-bit integer 2^kq * q in qd[dg].
       float qv[KS][16];
       if (hvalid) {
         const float* qp = q + (size_t(row) * a.q_heads + head) * D + 16u * g;
@@ -253,7 +253,7 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
       amax = rows_max(amax);
       int kq = 0;
       if (amax > 0.f) {
-        kq = 21 - __builtin_amdgcn_frexp_expf(amax);
+        kq = 22 - __builtin_amdgcn_frexp_expf(amax);  // |2^kq q| < 2^22: top digit in [-64, 64]
         kq = kq < -100 ? -100 : (kq > 100 ? 100 : kq);
       }
 #pragma unroll
@@ -263,7 +263,7 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
         for (int i = 0; i < 4; ++i) w[0][i] = w[1][i] = w[2][i] = 0u;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          int qi = int(__builtin_rintf(__builtin_amdgcn_ldexpf(qv[s][i], kq)));  // |qi| <= 2^21
+          int qi = int(__builtin_rintf(__builtin_amdgcn_ldexpf(qv[s][i], kq)));  // |qi| <= 2^22
           if (a.scale < 0.f) qi = -qi;  // scores scale by |scale| (see cs)
           const int lo8 = __builtin_amdgcn_sbfe(qi, 0, 8);
           const int r1 = (qi - lo8) >> 8;
@@ -392,7 +392,7 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
         const float vmax = wave_max(vm);
         int kp = 0;
         if (vmax > 0.f) {
-          kp = 20 - __builtin_amdgcn_frexp_expf(vmax);
+          kp = 21 - __builtin_amdgcn_frexp_expf(vmax * kVmaxMargin);
           kp = kp < -100 ? -100 : (kp > 100 ? 100 : kp);
         }
         const float f = m_run == neg_inf() ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -424,7 +424,7 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
                 lw += w;
                 float vsl = __uint_as_float(vsr[j][mb][e]);
                 if constexpr (MASK) vsl = 16u * g + 4u * mb + e < vlim ? vsl : 0.f;  // slots past the data
-                // p = w * v_scale rounded to an integer (|p| < 2^20) in one fma:
+                // p = w * v_scale rounded to an integer (0 <= p < 2^21) in one fma:
                 // 1.5 * 2^23 + p lies in [2^23, 2^24), where the float's ulp is
                 // 1, so its low 22 bits are p mod 2^22 (two's complement), and
                 // bits 0-6, 7-13 and 14-21 are the three digits of p.

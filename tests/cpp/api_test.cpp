@@ -1,12 +1,20 @@
-// Host-only check of the C++ face of libkvbridge_amd.so: the reference API
-// names and signatures (include/kvbridge/attention_shape.h,
-// attention_common.h) with the reference exception types
-// (src/attention_launch_checks.h:8-23).  Makes no device call: every launch
-// below is rejected on the host before anything is enqueued.
+// Check of the C++ face of libkvbridge_amd.so: the reference API names and
+// signatures (include/kvbridge/attention_shape.h, attention_common.h) with
+// the reference exception types (src/attention_launch_checks.h:8-23).
+// Without arguments it makes no device call: every launch below is rejected
+// on the host before anything is enqueued.  With --gpu it also calls the
+// three preload entry points (reference src/attention_shared.cu:376-387,
+// src/attention_mma.cu:13-31), which must return hipSuccess, and runs
+// launch_attention on a one-token cache, whose result is known exactly:
+// softmax over one visible token gives l = 1 and n = v_code * v_scale.
+#include <hip/hip_runtime.h>
+
 #include <cmath>
 #include <cstdio>
+#include <cstring>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "kvbridge/attention_ext.h"
 
@@ -30,7 +38,7 @@ static std::string invalid_message(F&& f) {
   return "<no exception>";
 }
 
-int main() {
+int main(int argc, char** argv) {
   const kvbridge::Shape base{8, 24, 4, 256, 32, 2048, 65536, 0, 65536, .0625f, true};
   expect(kvbridge::kSplitTokens == 256, "kSplitTokens");
   expect(kvbridge::attention_shape_valid(base), "valid base");
@@ -97,5 +105,61 @@ int main() {
          "append dim message");
   if (failures) return 1;
   std::printf("PASS C++ API host checks\n");
+  if (argc > 1 && std::strcmp(argv[1], "--gpu") == 0) {
+    expect(kvbridge::preload_attention_reference_kernels() == hipSuccess, "preload_attention_reference_kernels");
+    expect(kvbridge::preload_attention_mma_kernels() == hipSuccess, "preload_attention_mma_kernels");
+    expect(kvbridge::preload_attention_kernels() == hipSuccess, "preload_attention_kernels");
+    // One token, one kv head, two query heads, dim 64, page 16: softmax over
+    // the single visible token is exactly 1, so l = 1 and n[d] = v[d] * vs.
+    const kvbridge::Shape one{1, 2, 1, 64, 16, 1, 1, 0, 1, 0.125f, true};
+    std::vector<float> hq(2 * 64, 0.5f);
+    const int64_t qpos = 0, kpos = 0;
+    const uint32_t table = 0;
+    std::vector<int8_t> hk(16 * 64, 3), hv(64 * 16, 0);
+    for (int d = 0; d < 64; ++d) hv[d * 16] = int8_t(d - 32);  // slot 0 of dim-major V
+    std::vector<float> hks(16, 0.25f), hvs(16, 0.5f);
+    float *q, *ks, *vs, *sc, *m, *l, *n;
+    int64_t *qp, *kp;
+    uint32_t* tb;
+    int8_t *k, *v;
+    bool ok = hipMalloc(&q, hq.size() * 4) == hipSuccess && hipMalloc(&ks, 64) == hipSuccess &&
+              hipMalloc(&vs, 64) == hipSuccess && hipMalloc(&qp, 8) == hipSuccess && hipMalloc(&kp, 8) == hipSuccess &&
+              hipMalloc(&tb, 4) == hipSuccess && hipMalloc(&k, hk.size()) == hipSuccess &&
+              hipMalloc(&v, hv.size()) == hipSuccess && hipMalloc(&sc, kvbridge::scratch_elements(one) * 4) == hipSuccess &&
+              hipMalloc(&m, 8) == hipSuccess && hipMalloc(&l, 8) == hipSuccess && hipMalloc(&n, 2 * 64 * 4) == hipSuccess;
+    expect(ok, "device allocations");
+    if (!ok) return 1;
+    hipMemcpy(q, hq.data(), hq.size() * 4, hipMemcpyHostToDevice);
+    hipMemcpy(ks, hks.data(), 64, hipMemcpyHostToDevice);
+    hipMemcpy(vs, hvs.data(), 64, hipMemcpyHostToDevice);
+    hipMemcpy(qp, &qpos, 8, hipMemcpyHostToDevice);
+    hipMemcpy(kp, &kpos, 8, hipMemcpyHostToDevice);
+    hipMemcpy(tb, &table, 4, hipMemcpyHostToDevice);
+    hipMemcpy(k, hk.data(), hk.size(), hipMemcpyHostToDevice);
+    hipMemcpy(v, hv.data(), hv.size(), hipMemcpyHostToDevice);
+    const kvbridge::DeviceInput in{q, qp, kp, tb, k, v, ks, vs};
+    try {
+      kvbridge::launch_attention(one, in, sc, m, l, n, nullptr);
+    } catch (const std::exception& e) {
+      std::fprintf(stderr, "launch_attention threw: %s\n", e.what());
+      ++failures;
+    }
+    expect(hipDeviceSynchronize() == hipSuccess, "device synchronize");
+    float hm[2], hl[2], hn[128];
+    hipMemcpy(hm, m, 8, hipMemcpyDeviceToHost);
+    hipMemcpy(hl, l, 8, hipMemcpyDeviceToHost);
+    hipMemcpy(hn, n, sizeof(hn), hipMemcpyDeviceToHost);
+    const float score = 0.125f * 64 * 0.5f * 3 * 0.25f;  // scale * sum_d q * k_code * k_scale
+    for (int h = 0; h < 2; ++h) {
+      expect(std::fabs(hm[h] - score) <= 1e-5f * score, "m is the single token's score");
+      expect(hl[h] == 1.0f, "l = 1");
+      for (int d = 0; d < 64; ++d) expect(hn[h * 64 + d] == float(d - 32) * 0.5f, "n = v_code * v_scale");
+    }
+    for (void* p : {(void*)q, (void*)ks, (void*)vs, (void*)qp, (void*)kp, (void*)tb, (void*)k, (void*)v, (void*)sc,
+                    (void*)m, (void*)l, (void*)n})
+      hipFree(p);
+    if (failures) return 1;
+    std::printf("PASS C++ API device checks\n");
+  }
   return 0;
 }

@@ -61,7 +61,7 @@ def test_fused_matches_oracle_and_two_launch(gpu, cfg):
     counters = torch.zeros(kvh, dtype=torch.int32, device=gpu)
     ref = O.fp64(case, threads=8)
     mln, out = run_fused(dc, st, counters)
-    check_against_oracle(case, mln, "fused m/l/n", ref)
+    check_against_oracle(case, mln, "fused m/l/n", ref, strict=True)
     assert torch.count_nonzero(counters).item() == 0, "counters not left zero"
     (m2, l2, n2), out2, _ = dc.run_decode(st)
     m, l, n = mln

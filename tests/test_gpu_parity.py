@@ -3,7 +3,10 @@
 Gate (asserted): max-abs <= 2e-3 and relative L2 <= 1e-3 on the normalized
 output n/l, identical visibility, and the empty-row convention (m = -inf,
 l = 0, n = 0).  The reference's stricter per-element gate
-|a - r| <= 3e-6 + 5e-5|r| (examples/attention_bench.cu:127) is printed.
+|a - r| <= 3e-6 + 5e-5|r| (examples/attention_bench.cu:127) is asserted on the
+fp32 outputs of the cases below that use the configs' input distributions;
+it is reported only where an fp16 output or a wide-dynamic-range Q makes it
+unreachable by construction (see the cases).
 """
 import zlib
 
@@ -53,12 +56,13 @@ def test_reference_self_test_cases(gpu, i):
     ref = O.fp64(f, threads=8)
     assert kvb.attention_mma_supported(f.shape)
     a, _ = dc.run_reference_api(mma=False)
-    check_against_oracle(f, a, f"{name} launch_attention", ref)
+    check_against_oracle(f, a, f"{name} launch_attention", ref, strict=True)
     b, _ = dc.run_reference_api(mma=True)
-    check_against_oracle(f, b, f"{name} launch_attention_mma", ref)
-    # Bitwise repeatability of raw m/l/n (attention_bench.cu:179-181).
+    check_against_oracle(f, b, f"{name} launch_attention_mma", ref, strict=True)
+    # Bitwise repeatability of raw m/l/n of both entry points (attention_bench.cu:179-181).
     a2, _ = dc.run_reference_api(mma=False)
-    for x, y in zip(a, a2):
+    b2, _ = dc.run_reference_api(mma=True)
+    for x, y in list(zip(a, a2)) + list(zip(b, b2)):
         assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
 
 
@@ -70,11 +74,11 @@ def test_cfg1_decode(gpu):
     assert kvb.selected_kernel(case.shape, inp, st) == kvb.KVB_KERNEL_TILED_MFMA
     ref = O.fp64(case, threads=8)
     mln, out, _ = dc.run_decode(st, kvb.KVB_OUT_F32)
-    check_against_oracle(case, mln, "cfg1 decode m/l/n", ref)
+    check_against_oracle(case, mln, "cfg1 decode m/l/n", ref, strict=True)
     g = O.gates(out, ref[0])
-    assert g["pass"], g
+    assert g["pass"] and g["strict_pass"], g
     mln2, _ = dc.run_reference_api()
-    check_against_oracle(case, mln2, "cfg1 launch_attention", ref)
+    check_against_oracle(case, mln2, "cfg1 launch_attention", ref, strict=True)
 
 
 def test_cfg2_decode_full(gpu):
@@ -84,12 +88,12 @@ def test_cfg2_decode_full(gpu):
     assert kvb.selected_kernel(case.shape, dc.inp, st) == kvb.KVB_KERNEL_TILED_MFMA
     ref = O.fp64(case, threads=8)
     mln, out, _ = dc.run_decode(st, kvb.KVB_OUT_F16)
-    check_against_oracle(case, mln, "cfg2 decode m/l/n", ref)
+    check_against_oracle(case, mln, "cfg2 decode m/l/n", ref, strict=True)
     g = O.gates(out, ref[0])
     log(f"  cfg2 fp16 out: max_abs={g['max_abs']:.3e} rel_l2={g['rel_l2']:.3e}")
-    assert g["pass"], g
+    assert g["pass"], g  # fp16 output: its rounding (~5e-4 relative) is above the per-element gate
     mln2, _ = dc.run_reference_api()
-    check_against_oracle(case, mln2, "cfg2 launch_attention (256-token splits)", ref)
+    check_against_oracle(case, mln2, "cfg2 launch_attention (256-token splits)", ref, strict=True)
 
 
 RANDOM_SHAPES = [
@@ -115,9 +119,9 @@ def test_tiled_shapes(gpu, cfg):
     assert kvb.selected_kernel(case.shape, dc.inp, st) == kvb.KVB_KERNEL_TILED_MFMA
     ref = O.fp64(case, threads=8)
     mln, out, _ = dc.run_decode(st)
-    check_against_oracle(case, mln, f"decode split_tokens={st}", ref)
+    check_against_oracle(case, mln, f"decode split_tokens={st}", ref, strict=True)
     mln2, _ = dc.run_reference_api()
-    check_against_oracle(case, mln2, "launch_attention", ref)
+    check_against_oracle(case, mln2, "launch_attention", ref, strict=True)
 
 
 I8_ROWS_SHAPES = [
@@ -162,11 +166,20 @@ def test_i8_rows_kernel_shapes(gpu, cfg):
     assert name.startswith("split_i8_rows_kernel<"), name
     dc = DeviceCase(case)
     ref = O.fp64(case, threads=8)
+    # The per-element gate is asserted wherever the fp32 restatement of the
+    # reference's own split-K + merge algorithm meets it on the same input;
+    # with 8x outlier tokens it does not (its fp32 accumulation alone exceeds
+    # 3e-6 + 5e-5|r| on small outputs), and there the error is only reported.
+    sc32, ns32 = O.split_fp32(case, st, threads=8)
+    o32, _, _ = O.normalize(*O.merge_fp32(case.shape, sc32, ns32), d)
+    g32 = O.gates(o32, ref[0])
+    strict = bool(g32["strict_pass"])
+    log(f"  fp32 restatement: max_abs={g32['max_abs']:.3e} strict={'PASS' if strict else 'fail'}")
     mln, _, _ = dc.run_decode(st)
-    check_against_oracle(case, mln, f"decode split_tokens={st}", ref)
+    check_against_oracle(case, mln, f"decode split_tokens={st}", ref, strict=strict)
     mma = kvb.attention_mma_supported(case.shape)
     mln2, _ = dc.run_reference_api(mma=mma)
-    check_against_oracle(case, mln2, "launch_attention_mma" if mma else "launch_attention", ref)
+    check_against_oracle(case, mln2, "launch_attention_mma" if mma else "launch_attention", ref, strict=strict)
     mln3, _, _ = dc.run_decode(st)
     for x, y in zip(mln, mln3):  # bitwise repeatable
         assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
@@ -233,9 +246,9 @@ def test_generic_shapes(gpu, cfg):
     assert kvb.selected_kernel(case.shape, dc.inp, st) == kvb.KVB_KERNEL_GENERIC
     ref = O.fp64(case, threads=8)
     mln, out, _ = dc.run_decode(st)
-    check_against_oracle(case, mln, f"decode split_tokens={st}", ref)
+    check_against_oracle(case, mln, f"decode split_tokens={st}", ref, strict=True)
     mln2, _ = dc.run_reference_api()
-    check_against_oracle(case, mln2, "launch_attention", ref)
+    check_against_oracle(case, mln2, "launch_attention", ref, strict=True)
 
 
 def test_split_size_invariance(gpu):
@@ -246,7 +259,7 @@ def test_split_size_invariance(gpu):
     outs = []
     for st in (64, 256, 1024, 8192):
         mln, out, _ = dc.run_decode(st)
-        check_against_oracle(case, mln, f"split_tokens={st}", ref)
+        check_against_oracle(case, mln, f"split_tokens={st}", ref, strict=True)
         outs.append(out)
     for o in outs[1:]:
         assert np.max(np.abs(o - outs[0])) < 1e-4
@@ -298,3 +311,52 @@ def test_merge_attention_matches_oracle_merge(gpu, cfg):
                                    (n_ref, n64, nb, "oracle n")):
         err = np.abs(got.astype(np.float64) - want)
         assert np.all(err <= bound), f"{name}: worst error / bound {np.max(err / bound):.3g}"
+
+
+WIDE_Q_SHAPES = [
+    # rows, q_heads, kv_heads, dim, P, tokens, split_tokens, kernel family
+    (1, 32, 8, 128, 64, 8192, 2048, "split_i8_kernel<"),     # cfg2 geometry (paired-row QK)
+    (1, 8, 2, 64, 16, 512, 128, "split_i8_kernel<"),         # cfg1 geometry (small-page path)
+    (1, 64, 8, 128, 64, 4096, 1024, "split_i8_kernel<"),     # 8 head-rows per kv head
+    (8, 24, 4, 256, 32, 2048, 256, "split_i8_rows_kernel<"),  # dense rows-8 / group-6 geometry
+]
+
+
+@pytest.mark.parametrize("massive", [1e2, 1e3])
+@pytest.mark.parametrize("cfg", WIDE_Q_SHAPES)
+def test_wide_dynamic_range_q(gpu, cfg, massive):
+    """Q with one massive activation per head-row (+-massive in one dim, the
+    rest ~N(0, 1e-2), all fp16 values) through the int8-digit kernels, whose
+    only inexact input step is Q -> a 23-bit integer per head-row (a
+    component's rounding error is at most 2^-22 of the row's largest
+    magnitude).  The north-star gate is asserted for the two-launch and the
+    single-launch calls; the per-element gate is reported (a component 1e5
+    times below the row maximum keeps only a few of its bits)."""
+    import torch
+
+    rows, qh, kvh, d, p, t, st, family = cfg
+    seed = zlib.crc32(repr((cfg, massive)).encode()) & 0xFFFF
+    case = W.synth_case(rows, qh, kvh, d, p, t, seed=seed)
+    rng = np.random.default_rng(seed)
+    q = (rng.standard_normal((rows * qh, d)) * 1e-2).astype(np.float16)
+    big = rng.integers(0, d, size=rows * qh)
+    q[np.arange(rows * qh), big] = np.where(rng.random(rows * qh) < 0.5, -massive, massive)
+    case.q = q.astype(np.float32).ravel()
+    dc = DeviceCase(case)
+    name = kvb.selected_kernel_name(case.shape, dc.inp, st)
+    log(f"wide-range Q massive={massive} shape={case.shape.as_tuple()} split_tokens={st} kernel={name}")
+    assert name.startswith(family), name
+    ref = O.fp64(case, threads=8)
+    mln, _, _ = dc.run_decode(st)
+    g = check_against_oracle(case, mln, f"decode massive={massive}", ref)
+    if kvb.selected_kernel_name(case.shape, dc.inp, st, fused=True) != name:  # a single-launch kernel exists
+        counters = torch.zeros(kvh, dtype=torch.int32, device=gpu)
+        out = torch.full((rows * qh * d,), float("nan"), dtype=torch.float32, device=gpu)
+        kvb.decode_attention_fused(case.shape, dc.inp, st, dc.scratch(st), counters, dc.m, dc.l, dc.n, out,
+                                   kvb.KVB_OUT_F32)
+        torch.cuda.synchronize()
+        check_against_oracle(case, dc.read(), f"fused massive={massive}", ref)
+        assert torch.count_nonzero(counters).item() == 0
+    mln2, _ = dc.run_reference_api(mma=kvb.attention_mma_supported(case.shape))
+    check_against_oracle(case, mln2, f"reference entry massive={massive}", ref)
+    log(f"  measured: max_abs={g['max_abs']:.3e} rel_l2={g['rel_l2']:.3e}")
