@@ -164,6 +164,14 @@ def decode_attention_fused(s: Shape, inp: DeviceInput, split_tokens: int, scratc
                                             _stream(stream)))
 
 
+def decode_attention_noalloc(s: Shape, inp: DeviceInput, split_tokens: int, m, l, n, out=None,
+                             out_type: int = KVB_OUT_NONE, stream=None) -> None:
+    """Single-launch decode with the library's fixed 8 MiB per-device scratch
+    (kvb_decode_attention_noalloc): no caller scratch or counters, no allocation."""
+    check(load().kvb_decode_attention_noalloc(ctypes.byref(s), ctypes.byref(inp), split_tokens, _ptr(m), _ptr(l),
+                                              _ptr(n), _ptr(out), out_type, _stream(stream)))
+
+
 def selected_kernel(s: Shape, inp: DeviceInput, split_tokens: int) -> int:
     return load().kvb_selected_kernel(ctypes.byref(s), ctypes.byref(inp), split_tokens)
 

@@ -145,6 +145,11 @@ bool batch_uses_i8(const kvbridge::BatchShape& b, const kvb_batch_input& in, con
 
 namespace kvb {
 
+int set_error(int code, const std::string& msg) {
+  g_error = msg;
+  return code;
+}
+
 SplitArgs make_split_args(const kvbridge::Shape& s, const kvbridge::DeviceInput& in,
                           unsigned split_tokens, unsigned splits, float* scratch) {
   SplitArgs a{};

@@ -3,6 +3,7 @@
 #pragma once
 #include <hip/hip_runtime_api.h>
 #include <cstdint>
+#include <string>
 #include "kvbridge/attention_common.h"
 
 namespace kvb {
@@ -46,6 +47,9 @@ struct SplitArgs {
   uint32_t table_entries;        // page_table entries (likewise)
   uint32_t max_tokens;           // bound on every sequence's token count
 };
+
+// Sets the thread-local message kvb_last_error() returns; returns code.
+int set_error(int code, const std::string& msg);
 
 SplitArgs make_split_args(const kvbridge::Shape& s, const kvbridge::DeviceInput& in,
                           unsigned split_tokens, unsigned splits, float* scratch);
