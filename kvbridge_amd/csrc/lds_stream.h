@@ -207,6 +207,101 @@ __device__ __forceinline__ void pt_issue(const PtCtx& c, uint32_t slab, uint32_t
   __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rvs, (lds_ptr)(sb + 256), 4, c.voff_s, sbase, 0, 0);
 }
 
+// ---- one tile's DMA shared by WT waves: wave `part` issues the K and V
+// loads i with i % WT == part, part 0 also the k-scales and part 1 the
+// v-scales (WT == 1: one wave issues everything), so a wave holds the
+// per-lane offsets of its own loads only and issuing costs each wave a
+// WT-th of the instructions.
+template <int D, uint32_t WT>
+struct PtPart {
+  static_assert(WT >= 1 && Geo<D>::kChunks % WT == 0 && (D / 16) % WT == 0, "whole shares");
+  static constexpr uint32_t kK = Geo<D>::kChunks / WT;  // K loads of one wave
+  static constexpr uint32_t kV = (D / 16) / WT;         // V loads of one wave
+  __amdgpu_buffer_rsrc_t rk, rv, rks, rvs;
+  uint32_t voff_k[kK];
+  uint32_t voff_v, voff_s;
+};
+
+template <int D, uint32_t WT>
+__device__ __forceinline__ void pt_part_init(PtPart<D, WT>& c, const int8_t* k, const int8_t* v, const float* ks,
+                                             const float* vs, uint32_t kv_bytes, uint32_t scale_bytes, uint32_t P,
+                                             uint32_t lane, uint32_t part) {
+  using G = Geo<D>;
+  c.rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(k), 0, int(kv_bytes), kRsrcFlags);
+  c.rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(v), 0, int(kv_bytes), kRsrcFlags);
+  c.rks = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(ks), 0, int(scale_bytes), kRsrcFlags);
+  c.rvs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vs), 0, int(scale_bytes), kRsrcFlags);
+#pragma unroll
+  for (uint32_t m = 0; m < PtPart<D, WT>::kK; ++m) {
+    const uint32_t r = (part + WT * m) * G::kRowsPerLoad + lane / G::kChunks;
+    c.voff_k[m] = r * D + 16u * ((lane % G::kChunks) ^ swz_k<D>(r));
+  }
+  const uint32_t d = lane >> 2;
+  c.voff_v = d * P + 16u * ((lane & 3u) ^ swz_v(d));
+  c.voff_s = 4u * lane;
+}
+
+// Page-tile path (a tile lies in one page): this wave's share of the tile
+// whose first K row is row `slot0` of slab `slab`.
+template <int D, uint32_t WT>
+__device__ __forceinline__ void pt_part_issue(const PtPart<D, WT>& c, uint32_t slab, uint32_t slot0, uint32_t P,
+                                              uint8_t* buf, uint32_t part) {
+  using G = Geo<D>;
+  const uint32_t kbase = (slab * P + slot0) * D;
+#pragma unroll
+  for (uint32_t m = 0; m < PtPart<D, WT>::kK; ++m)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rk, (lds_ptr)(buf + 1024u * (part + WT * m)), 16, c.voff_k[m], kbase,
+                                             0, 0);
+  const uint32_t vbase = slab * D * P + slot0;
+  uint8_t* vb = buf + G::kKBytes;
+#pragma unroll
+  for (uint32_t m = 0; m < PtPart<D, WT>::kV; ++m) {
+    const uint32_t i = part + WT * m;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rv, (lds_ptr)(vb + 1024u * i), 16, c.voff_v, vbase + 16u * i * P, 0, 0);
+  }
+  uint8_t* sb = buf + G::kKBytes + G::kVBytes;
+  if (WT == 1u || part == 0u)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rks, (lds_ptr)(sb), 4, c.voff_s, (slab * P + slot0) * 4u, 0, 0);
+  if (WT == 1u || part == 1u)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rvs, (lds_ptr)(sb + 256), 4, c.voff_s, (slab * P + slot0) * 4u, 0, 0);
+}
+
+// Any page size: this wave's share of tile `tile` (pages of its four
+// 16-token groups from the page-table window).
+template <int D, uint32_t WT>
+__device__ __forceinline__ void part_issue(const Ctx& c, uint32_t tile, uint8_t* buf, uint32_t part) {
+  using G = Geo<D>;
+  const Pages4 pg = tile_pages(c, tile);
+  const uint32_t t0 = tile * kTileTokens;
+  const uint32_t lane = c.lane;
+#pragma unroll
+  for (uint32_t m = 0; m < PtPart<D, WT>::kK; ++m) {
+    const uint32_t i = part + WT * m;
+    const uint32_t r = i * G::kRowsPerLoad + lane / G::kChunks;
+    const uint32_t chunk = (lane % G::kChunks) ^ swz_k<D>(r);
+    const uint32_t grp = r >> 4;
+    const uint32_t row = (pick4(pg, grp) * c.kv_heads + c.kv) * c.P + (t0 + 16u * grp) % c.P + (r & 15u);
+    __builtin_amdgcn_global_load_lds(c.k + size_t(row) * D + 16u * chunk, (lds_ptr)(buf + 1024u * i), 16, 0, 0);
+  }
+  uint8_t* vb = buf + G::kKBytes;
+#pragma unroll
+  for (uint32_t m = 0; m < PtPart<D, WT>::kV; ++m) {
+    const uint32_t i = part + WT * m;
+    const uint32_t d = 16u * i + (lane >> 2);
+    const uint32_t grp = (lane & 3u) ^ swz_v(d);
+    const uint32_t slab = pick4(pg, grp) * c.kv_heads + c.kv;
+    __builtin_amdgcn_global_load_lds(c.v + (size_t(slab) * D + d) * c.P + (t0 + 16u * grp) % c.P,
+                                     (lds_ptr)(vb + 1024u * i), 16, 0, 0);
+  }
+  if (WT == 1u || part < 2u) {
+    const uint32_t grp = lane >> 4;
+    const uint32_t si = (pick4(pg, grp) * c.kv_heads + c.kv) * c.P + (t0 + 16u * grp) % c.P + (lane & 15u);
+    uint8_t* sb = buf + G::kKBytes + G::kVBytes;
+    if (WT == 1u || part == 0u) __builtin_amdgcn_global_load_lds(c.ks + si, (lds_ptr)(sb), 4, 0, 0);
+    if (WT == 1u || part == 1u) __builtin_amdgcn_global_load_lds(c.vs + si, (lds_ptr)(sb + 256), 4, 0, 0);
+  }
+}
+
 // Position of the next tile to issue: (logical page, slot of its first token),
 // advanced without division; clamped at the split's last tile.
 struct IssuePos {

@@ -5,11 +5,18 @@
 // One work-group of four waves per (split, kv head) streams the split's KV
 // tiles through a two-slot LDS ring (CT tiles per slot: the tile images of
 // lds_stream.h), and wave w runs head-row block w (16 head-rows) over each
-// tile, so the split's KV is read from HBM once for all its head-rows.
-// While the waves compute phase p (slot p & 1), the DMA of phase p + 1 is in
-// flight; phase p + 2 is issued into the slot after the barrier that ends
-// phase p.  More than 64 head-rows (four blocks) stream the split again per
-// group of four blocks.
+// tile, so the split's KV is read from HBM once for all its head-rows.  More
+// than 64 head-rows (four blocks) stream the split again per group of four
+// blocks.  The DMA runs one phase ahead of the compute:
+//  - fewer blocks than waves (one round, e.g. 48 head-rows): the idle wave
+//    issues every tile's DMA alone, phase p + 1 right after the barrier that
+//    starts phase p (every wave is then done with its slot), so a busy memory
+//    system's issue stalls never hold up a computing wave, and one barrier
+//    per phase suffices;
+//  - otherwise the waves share each tile's DMA and issue phase p + 2 after a
+//    second barrier that ends phase p.
+// The prologue's own loads (Q, positions) go out before the first DMA, so
+// its waits do not include it.
 //
 // Per phase, wave-local and exact in integers as in the single-block int8
 // kernel (split_i8.h):
@@ -25,6 +32,13 @@
 //    its k-positions of PV), so nothing moves between lanes.  Each 16-dim
 //    block's three int32 digit sums over the phase are folded into fp32 at
 //    once (2^-kp).
+// QK and PV are software-pipelined over their 16-row / 16-dim blocks: a
+// block's LDS reads go out two blocks ahead (issued without a wait; the
+// wait is a separate statement and the results are pinned after it), and a
+// block's MFMAs are interleaved with the previous block's VALU work (scores,
+// or the fold), so the matrix core, the VALU and the LDS work at once with
+// one wave per SIMD.  Branches that would split those scheduling regions
+// (masking) are taken once per phase.
 // A wave owns whole head-rows and writes their partials from registers.
 // Requires splits that start on a 64-token tile (host-checked).
 #include <atomic>
@@ -41,7 +55,8 @@ namespace {
 using namespace lds;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4;
+constexpr int kBlocks = 4;  // head-row blocks per round, one wave each
+constexpr int kWaves = kBlocks;
 constexpr float kLn2 = 0.6931471805599453f;
 
 // LDS reads as one asm statement each: the reads and the wait for them, so
@@ -79,6 +94,96 @@ __device__ __forceinline__ uint32_t ds_read4_sync(uint32_t a) {
   return r;
 }
 
+// K rows of one QK M-block over KS K-steps (one address per K-step, same
+// immediate) plus the block's four k-scales, in one statement.
+template <uint32_t OK, uint32_t OS>
+__device__ __forceinline__ void ds_read_kblock(const uint32_t (&a)[4], uint32_t as, u32x4_t (&r)[4], u32x4_t& rs) {
+  asm volatile(
+      "ds_read_b128 %0, %5 offset:%10\n\t"
+      "ds_read_b128 %1, %6 offset:%10\n\t"
+      "ds_read_b128 %2, %7 offset:%10\n\t"
+      "ds_read_b128 %3, %8 offset:%10\n\t"
+      "ds_read_b128 %4, %9 offset:%11\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(rs)
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(as), "i"(OK), "i"(OS)
+      : "memory");
+}
+template <uint32_t OK, uint32_t OS>
+__device__ __forceinline__ void ds_read_kblock(const uint32_t (&a)[2], uint32_t as, u32x4_t (&r)[2], u32x4_t& rs) {
+  asm volatile(
+      "ds_read_b128 %0, %3 offset:%6\n\t"
+      "ds_read_b128 %1, %4 offset:%6\n\t"
+      "ds_read_b128 %2, %5 offset:%7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(rs)
+      : "v"(a[0]), "v"(a[1]), "v"(as), "i"(OK), "i"(OS)
+      : "memory");
+}
+
+// LDS reads issued without a wait (the wait is a separate statement, and
+// every use of the results comes after it, pinned there; the kernels'
+// assembly is checked for early uses by check_lds_waits.py).
+template <uint32_t O0, uint32_t O1>
+__device__ __forceinline__ void ds_issue16x2(uint32_t a, u32x4_t& r0, u32x4_t& r1) {
+  asm volatile(
+      "ds_read_b128 %0, %2 offset:%3\n\t"
+      "ds_read_b128 %1, %2 offset:%4"
+      : "=&v"(r0), "=&v"(r1)
+      : "v"(a), "i"(O0), "i"(O1)
+      : "memory");
+}
+template <uint32_t O0, uint32_t O1, uint32_t O2, uint32_t O3>
+__device__ __forceinline__ void ds_issue16x4(uint32_t a, u32x4_t& r0, u32x4_t& r1, u32x4_t& r2, u32x4_t& r3) {
+  asm volatile(
+      "ds_read_b128 %0, %4 offset:%5\n\t"
+      "ds_read_b128 %1, %4 offset:%6\n\t"
+      "ds_read_b128 %2, %4 offset:%7\n\t"
+      "ds_read_b128 %3, %4 offset:%8"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+      : "v"(a), "i"(O0), "i"(O1), "i"(O2), "i"(O3)
+      : "memory");
+}
+// ds_read_kblock without the wait.
+template <uint32_t OK, uint32_t OS>
+__device__ __forceinline__ void ds_issue_kblock(const uint32_t (&a)[4], uint32_t as, u32x4_t (&r)[4], u32x4_t& rs) {
+  asm volatile(
+      "ds_read_b128 %0, %5 offset:%10\n\t"
+      "ds_read_b128 %1, %6 offset:%10\n\t"
+      "ds_read_b128 %2, %7 offset:%10\n\t"
+      "ds_read_b128 %3, %8 offset:%10\n\t"
+      "ds_read_b128 %4, %9 offset:%11"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(rs)
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(as), "i"(OK), "i"(OS)
+      : "memory");
+}
+template <uint32_t OK, uint32_t OS>
+__device__ __forceinline__ void ds_issue_kblock(const uint32_t (&a)[2], uint32_t as, u32x4_t (&r)[2], u32x4_t& rs) {
+  asm volatile(
+      "ds_read_b128 %0, %3 offset:%6\n\t"
+      "ds_read_b128 %1, %4 offset:%6\n\t"
+      "ds_read_b128 %2, %5 offset:%7"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(rs)
+      : "v"(a[0]), "v"(a[1]), "v"(as), "i"(OK), "i"(OS)
+      : "memory");
+}
+template <uint32_t N>
+__device__ __forceinline__ void wait_lgkm() { asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory"); }
+
+// Pins a value at this point of the instruction stream: its producers stay
+// before, its users after (keeps each block's VALU next to its MFMAs
+// instead of letting the compiler sink it, which lengthens live ranges).
+template <class T>
+__device__ __forceinline__ void pin(T& v) {
+  if constexpr (sizeof(T) == 16) {
+    u32x4_t x = __builtin_bit_cast(u32x4_t, v);
+    asm volatile("" : "+v"(x));
+    v = __builtin_bit_cast(T, x);
+  } else {
+    asm volatile("" : "+v"(v));
+  }
+}
+
 template <int D>
 struct RowsGeo {
   static constexpr int kCT = D == 256 ? 2 : 4;  // tiles per phase (one LDS slot, about 66 KiB)
@@ -97,7 +202,7 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
   constexpr int KS = D / 64;  // K-steps of QK
   constexpr int MB = D / 16;  // 16-dim blocks of PV
   constexpr uint32_t W = D + 2;
-  static_assert(CT <= kWaves, "one tile per wave per phase");
+  static_assert(CT <= kWaves, "every tile of a phase has an issuing wave");
   static_assert(G::kLoadsPerTile <= 63, "vmcnt range");
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kSlot];
   const uint32_t lane = threadIdx.x & 63u;
@@ -105,7 +210,7 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
   const uint32_t n = lane & 15u, g = lane >> 4;
   const uint32_t kv = blockIdx.y;
   const uint32_t head_rows = a.rows * a.group, hblocks = (head_rows + 15u) / 16u;
-  const uint32_t rounds = (hblocks + kWaves - 1u) / kWaves;
+  const uint32_t rounds = (hblocks + kBlocks - 1u) / kBlocks;
 
   // Splits [sp0, sp1) of this work-group, tokens [s0, s1).  With spw > 1 a
   // split is a whole number of phases (pps; host-checked) and every split's
@@ -122,8 +227,13 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
   const uint32_t ntiles = s1 > s0 ? (s1 - 1u) / kTileTokens + 1u - k_first : 0u;
   const uint32_t nphase = (ntiles + CT - 1u) / CT;
 
+  // The DMA of each tile of a phase is shared by WT waves (wave w: tile
+  // w / WT of the phase, share w % WT).
+  constexpr uint32_t WT = kWaves / CT;
+  using Part = PtPart<D, WT>;
+  const uint32_t it_j = wave / WT, part = wave % WT;
   Ctx c;
-  PtCtx pc;
+  Part pc;
   if (ntiles > 0) {
     c.k = kdata;
     c.v = vdata;
@@ -142,23 +252,68 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
     if constexpr (PT) {
       const uint32_t kv_bytes = a.pages * a.kv_heads * a.page_tokens * uint32_t(D);
       const uint32_t sc_bytes = a.pages * a.kv_heads * a.page_tokens * 4u;
-      pt_init<D>(pc, kdata, vdata, kscale, vscale, kv_bytes, sc_bytes, a.page_tokens, lane);
+      pt_part_init<D, WT>(pc, kdata, vdata, kscale, vscale, kv_bytes, sc_bytes, a.page_tokens, lane, part);
     }
   }
-  // Tile p * CT + j of the split goes to slot p & 1, position j, by wave j.
-  auto issued = [&](uint32_t p) -> bool { return wave < uint32_t(CT) && p * CT + wave < ntiles; };
-  auto issue = [&](uint32_t p) {
-    if (!issued(p)) return;
-    uint8_t* const buf = smem + (p & 1u) * kSlot + wave * G::kBufBytes;
-    const uint32_t k = k_first + p * CT + wave;
+  // When the blocks leave a wave idle (fewer blocks than waves: one round),
+  // that wave issues every DMA of the split alone, so the issue stalls of a
+  // busy memory system never hold up a computing wave; otherwise the waves
+  // share each tile's DMA.
+  const bool idle_dma = hblocks < uint32_t(kBlocks);
+  const bool dma_wave = idle_dma && wave == uint32_t(kWaves - 1);
+  using Part1 = PtPart<D, 1>;
+  Part1 pc1;
+  if constexpr (PT) {
+    if (dma_wave && ntiles > 0) {
+      const uint32_t kv_bytes = a.pages * a.kv_heads * a.page_tokens * uint32_t(D);
+      const uint32_t sc_bytes = a.pages * a.kv_heads * a.page_tokens * 4u;
+      pt_part_init<D, 1>(pc1, kdata, vdata, kscale, vscale, kv_bytes, sc_bytes, a.page_tokens, lane, 0u);
+    }
+  }
+  // Tile p * CT + j of the split goes to slot p & 1, position j.
+  auto issued = [&](uint32_t p) -> bool {
+    return idle_dma ? dma_wave && p * CT < ntiles : p * CT + it_j < ntiles;
+  };
+  auto issue_tile_of = [&](auto wtc, const auto& ppc, uint32_t k, uint8_t* buf, uint32_t prt)
+                           __attribute__((always_inline)) {
+    constexpr uint32_t W2 = decltype(wtc)::value;
     if constexpr (PT) {
       const uint32_t lp = k * kTileTokens / a.page_tokens;
       const uint32_t rel = lp - c.lp_lo;
       uint32_t phys = rel < 64u ? __builtin_amdgcn_readlane(c.ptab, rel) : table[lp];
       phys = phys < a.pages ? phys : a.pages - 1u;
-      pt_issue<D>(pc, phys * a.kv_heads + kv, k * kTileTokens - lp * a.page_tokens, a.page_tokens, buf);
+      pt_part_issue<D, W2>(ppc, phys * a.kv_heads + kv, k * kTileTokens - lp * a.page_tokens, a.page_tokens, buf,
+                           prt);
     } else {
-      issue_tile<D>(c, k, buf);
+      part_issue<D, W2>(c, k, buf, prt);
+    }
+  };
+  auto issue = [&](uint32_t p) {
+    if (!issued(p)) return;
+    if (idle_dma) {
+      static_for<0, CT>([&](auto jc) __attribute__((always_inline)) {
+        constexpr uint32_t j = decltype(jc)::value;
+        if (p * CT + j < ntiles)
+          issue_tile_of(std::integral_constant<uint32_t, 1>{}, pc1, k_first + p * CT + j,
+                        smem + (p & 1u) * kSlot + j * G::kBufBytes, 0u);
+      });
+    } else {
+      issue_tile_of(std::integral_constant<uint32_t, WT>{}, pc, k_first + p * CT + it_j,
+                    smem + (p & 1u) * kSlot + it_j * G::kBufBytes, part);
+    }
+  };
+  // Before phase p: this wave's loads of phase p done, those of phase p + 1
+  // may stay in flight (shared issue: phase p + 1 went out at the end of
+  // phase p - 1; the DMA wave issues phase p + 1 only after this wait).
+  auto wait_next = [&](uint32_t p) __attribute__((always_inline)) {
+    if (idle_dma || !issued(p + 1u)) {
+      wait_vm<0>();
+    } else if (WT == 1u) {
+      wait_vm<Part::kK + Part::kV + 2>();
+    } else if (part < 2u) {
+      wait_vm<Part::kK + Part::kV + 1>();
+    } else {
+      wait_vm<Part::kK + Part::kV>();
     }
   };
 
@@ -181,12 +336,12 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
   const uint32_t vmoff = G::kKBytes + G::kVBytes + 256u + 4u * lane;
 
   for (uint32_t round = 0; round < rounds; ++round) {
-    const uint32_t hblock = wave + kWaves * round;
+    const uint32_t hblock = wave + kBlocks * round;
     const bool has = hblock < hblocks;  // wave-uniform
-    if (nphase > 0) issue(0);
-    if (nphase > 1) issue(1);
-
-    // ---- block prologue: visibility, Q digits
+    // ---- block prologue: visibility, Q digits.  The prologue's own requests
+    // (Q elements, the split's last key position, the block's query
+    // positions) go out before the first two phases' DMA, so its waits do not
+    // include the DMA.
     const uint32_t hr = hblock * 16u + n;
     const bool hvalid = hr < head_rows;
     const uint32_t row = hvalid ? hr / a.group : 0u;
@@ -194,39 +349,12 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
     uint32_t e_h = s0, e_min = s0, e_max = s0;
     i32x4 qd[3][KS];
     float cs = 0.f;
+    // lane (h, g) holds dims 64s + 16g .. +15 of head-row h
+    float qv[KS][16];
+    int64_t klast = 0, qpos_l = INT64_MAX;  // lane i: query position of row r_lo + i
+    const uint32_t r_lo = hblock * 16u / a.group;
+    const uint32_t r_hi = (hblock * 16u + 15u < head_rows ? hblock * 16u + 15u : head_rows - 1u) / a.group;
     if (has) {
-      if (s1 > s0) {
-        const uint32_t r_lo = hblock * 16u / a.group;
-        const uint32_t r_hi = (hblock * 16u + 15u < head_rows ? hblock * 16u + 15u : head_rows - 1u) / a.group;
-        const int64_t klast = kpos[s1 - 1u];
-        bool all_visible = true;
-        for (uint32_t r = r_lo; r <= r_hi; ++r) all_visible &= klast <= qpos[r];
-        if (all_visible) {
-          e_h = s1;
-        } else {
-          for (uint32_t r = r_lo; r <= r_hi; ++r) {
-            const uint32_t e = visible_end(kpos, s0, s1, qpos[r], lane);
-            if (row == r) e_h = e;
-          }
-        }
-        if (!hvalid) e_h = s0;
-      }
-      uint32_t lo = hvalid ? e_h : 0xffffffffu, hi = e_h;
-#define KVB_ROW_RED(N)                                                                                 \
-  {                                                                                                    \
-    const uint32_t o1 = uint32_t(__builtin_amdgcn_update_dpp(0, int(lo), 0x120 + N, 0xF, 0xF, false)); \
-    const uint32_t o2 = uint32_t(__builtin_amdgcn_update_dpp(0, int(hi), 0x120 + N, 0xF, 0xF, false)); \
-    lo = o1 < lo ? o1 : lo;                                                                            \
-    hi = o2 > hi ? o2 : hi;                                                                            \
-  }
-      KVB_ROW_RED(8) KVB_ROW_RED(4) KVB_ROW_RED(2) KVB_ROW_RED(1)
-#undef KVB_ROW_RED
-      e_min = __builtin_amdgcn_readfirstlane(lo);
-      e_max = __builtin_amdgcn_readfirstlane(hi);
-
-      // Q digits (B of QK): lane (h, g) holds dims 64s + 16g .. +15 of
-      // head-row h; digit dg of the 23-bit integer 2^kq * q in qd[dg].
-      float qv[KS][16];
       if (hvalid) {
         const float* qp = q + (size_t(row) * a.q_heads + head) * D + 16u * g;
 #pragma unroll
@@ -245,6 +373,42 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
 #pragma unroll
           for (int i = 0; i < 16; ++i) qv[s][i] = 0.f;
       }
+      if (s1 > s0) {
+        klast = kpos[s1 - 1u];
+        if (lane <= r_hi - r_lo) qpos_l = qpos[r_lo + lane];  // at most 16 rows per block
+      }
+    }
+    if (nphase > 0) issue(0);
+    if (nphase > 1 && !idle_dma) issue(1);  // (the DMA wave issues phase p + 1 at the start of phase p)
+    if (has) {
+      if (s1 > s0) {
+        if (__ballot(klast > qpos_l) == 0) {  // every row of the block sees the whole split
+          e_h = s1;
+        } else {
+          for (uint32_t r = r_lo; r <= r_hi; ++r) {
+            const uint64_t xb = uint64_t(qpos_l);
+            const uint32_t xlo = __builtin_amdgcn_readlane(uint32_t(xb), r - r_lo);
+            const uint32_t xhi = __builtin_amdgcn_readlane(uint32_t(xb >> 32), r - r_lo);
+            const uint32_t e = visible_end(kpos, s0, s1, int64_t((uint64_t(xhi) << 32) | xlo), lane);
+            if (row == r) e_h = e;
+          }
+        }
+        if (!hvalid) e_h = s0;
+      }
+      uint32_t lo = hvalid ? e_h : 0xffffffffu, hi = e_h;
+#define KVB_ROW_RED(N)                                                                                 \
+  {                                                                                                    \
+    const uint32_t o1 = uint32_t(__builtin_amdgcn_update_dpp(0, int(lo), 0x120 + N, 0xF, 0xF, false)); \
+    const uint32_t o2 = uint32_t(__builtin_amdgcn_update_dpp(0, int(hi), 0x120 + N, 0xF, 0xF, false)); \
+    lo = o1 < lo ? o1 : lo;                                                                            \
+    hi = o2 > hi ? o2 : hi;                                                                            \
+  }
+      KVB_ROW_RED(8) KVB_ROW_RED(4) KVB_ROW_RED(2) KVB_ROW_RED(1)
+#undef KVB_ROW_RED
+      e_min = __builtin_amdgcn_readfirstlane(lo);
+      e_max = __builtin_amdgcn_readfirstlane(hi);
+
+      // Q digits (B of QK): digit dg of the 23-bit integer 2^kq * q in qd[dg].
       float amax = 0.f;
 #pragma unroll
       for (int s = 0; s < KS; ++s)
@@ -286,7 +450,7 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
     const uint32_t nvis = has && e_max > s0 ? (e_max - 1u) / kTileTokens + 1u - k_first : 0u;  // tiles
 
     float m_run = neg_inf(), l_run = 0.f;  // per lane: head-row h's running max (log2) and partial sum
-    f32x4 acc[MB];
+    f32x4 acc[MB];  // lane (h, g): dims 16mb + 4g + e
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
     // This block's partial of split `split` from the registers (lane (h, g):
@@ -311,10 +475,16 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
       for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
     };
 
-    for (uint32_t p = 0; p < nphase; ++p) {
-      if (issued(p + 1u)) wait_vm<G::kLoadsPerTile>();
-      else wait_vm<0>();
-      __syncthreads();
+    // Splits of this work-group one after another (one split, or spw whole
+    // splits of pps phases each); the DMA pipeline runs across them.
+    const uint32_t ppsplit = spw > 1u ? pps : nphase;
+    for (uint32_t sp = sp0; sp < sp1; ++sp) {
+    const uint32_t p_lo = (sp - sp0) * ppsplit;
+    const uint32_t p_hi = p_lo + ppsplit < nphase ? p_lo + ppsplit : nphase;
+    for (uint32_t p = p_lo; p < p_hi; ++p) {
+      wait_next(p);
+      __syncthreads();  // phase p landed; every wave is done with phase p - 1 (slot (p + 1) & 1)
+      if (idle_dma && p + 1u < nphase) issue(p + 1u);  // the DMA wave, while the others compute
       const uint32_t tp = p * CT;  // first tile of the phase (split-relative)
       if (tp < nvis) {
         // LDS addresses of the slot (tile j adds j * kBufBytes as an immediate).
@@ -329,61 +499,93 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
         // (cs > 0, so maxima of y are maxima of scores).
         float sc[CT][16];
         float mx = neg_inf();
-        static_for<0, CT>([&](auto jc) __attribute__((always_inline)) {
-          constexpr uint32_t j = decltype(jc)::value;
-          constexpr uint32_t TB = j * G::kBufBytes;
+        // The phase's CT x 4 QK M-blocks (tile j = b / 4, block mb = b % 4) in
+        // one software pipeline: block b's reads went out two blocks earlier
+        // (three register sets), block b's MFMAs are interleaved with block
+        // b - 1's scores.  Every tile runs (a tile past the visible range is
+        // fully masked), so the pipeline has no branch.
+        constexpr uint32_t NB = CT * 4u;
+        constexpr uint32_t kRd = KS + 1u;  // LDS reads per block
+        u32x4_t kr[3][KS], ksr[3];
+        auto read_k = [&](auto bc) __attribute__((always_inline)) {
+          constexpr uint32_t bb = decltype(bc)::value;
+          constexpr uint32_t TB = (bb / 4u) * G::kBufBytes, mb = bb % 4u;
+          ds_issue_kblock<TB + 4u * mb * D, TB + 16u * mb>(ka, sa, kr[bb % 3u], ksr[bb % 3u]);
+        };
+        i32x4 cq[2][3];
+        u32x4_t ksc[2];  // k-scales of blocks b (set b & 1), copied before their registers are refilled
+        // Masking per phase, outside the pipeline (a branch inside it would
+        // split the scheduling regions that interleave MFMAs and VALU): a
+        // phase whose tiles every head-row of the block sees in full runs
+        // unmasked.
+        uint32_t vis[CT];
 #pragma unroll
-          for (int i = 0; i < 16; ++i) sc[j][i] = neg_inf();
-          if (tp + j >= nvis) return;
+        for (int j = 0; j < CT; ++j) {
           const uint32_t t0 = (k_first + tp + j) * kTileTokens;
-          u32x4_t ks[4];
-          ds_read16x4<TB, TB + 16u, TB + 32u, TB + 48u>(sa, ks[0], ks[1], ks[2], ks[3]);
-          i32x4 cq[3][4];
+          vis[j] = tp + j < nvis ? (e_h > t0 ? (e_h - t0 < kTileTokens ? e_h - t0 : kTileTokens) : 0u) : 0u;
+        }
+        const bool phase_full = tp + CT <= nvis && (k_first + tp + CT) * kTileTokens <= e_min;
+        auto qk = [&](auto maskc) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(maskc)::value;
+        auto scores = [&](auto bc) __attribute__((always_inline)) {
+          constexpr uint32_t bb = decltype(bc)::value;
+          constexpr uint32_t j = bb / 4u, mb = bb % 4u;
+          const i32x4(&c)[3] = cq[bb & 1u];
+          const u32x4_t ksm = ksc[bb & 1u];
 #pragma unroll
-          for (int mb = 0; mb < 4; ++mb)
+          for (int e = 0; e < 4; ++e) {
+            const int hi2 = c[0][e] * 256 + c[1][e];  // |.| < 2^29
+            float s2 = fmaf(float(hi2), 256.f, float(c[2][e])) * __uint_as_float(ksm[e]);
+            if constexpr (MASK) s2 = 16u * g + 4u * mb + e < vis[j] ? s2 : neg_inf();
+            sc[j][4 * mb + e] = s2;
+            mx = fmaxf(mx, s2);
+          }
 #pragma unroll
-            for (int dg = 0; dg < 3; ++dg) cq[dg][mb] = i32x4{0, 0, 0, 0};
-          static_for<0, KS>([&](auto sc_) __attribute__((always_inline)) {
-            constexpr uint32_t s = decltype(sc_)::value;
-            u32x4_t kr[4];
-            ds_read16x4<TB, TB + 4u * D, TB + 8u * D, TB + 12u * D>(ka[s], kr[0], kr[1], kr[2], kr[3]);
+          for (int e = 0; e < 4; ++e) pin(sc[j][4 * mb + e]);
+        };
+        read_k(std::integral_constant<uint32_t, 0>{});
+        read_k(std::integral_constant<uint32_t, 1>{});
+        static_for<0, NB>([&](auto bc) __attribute__((always_inline)) {
+          constexpr uint32_t bb = decltype(bc)::value;
+          // block bb's reads done; block bb + 1's may still be in flight
+          if constexpr (bb + 1 < NB) wait_lgkm<kRd>();
+          else wait_lgkm<0>();
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
-              const i32x4 av = {int(kr[mb][0]), int(kr[mb][1]), int(kr[mb][2]), int(kr[mb][3])};
+          for (int st = 0; st < KS; ++st) pin(kr[bb % 3u][st]);
+          pin(ksr[bb % 3u]);
+          ksc[bb & 1u] = ksr[bb % 3u];
+          if constexpr (bb + 2 < NB) read_k(std::integral_constant<uint32_t, bb + 2>{});
+          i32x4(&c)[3] = cq[bb & 1u];
 #pragma unroll
-              for (int dg = 0; dg < 3; ++dg)
-                cq[dg][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, qd[dg][s], cq[dg][mb], 0, 0, 0);
+          for (int dg = 0; dg < 3; ++dg) c[dg] = i32x4{0, 0, 0, 0};
+#pragma unroll
+          for (int st = 0; st < KS; ++st) {
+            const u32x4_t& k4 = kr[bb % 3u][st];
+            const i32x4 av = {int(k4[0]), int(k4[1]), int(k4[2]), int(k4[3])};
+#pragma unroll
+            for (int dg = 0; dg < 3; ++dg) c[dg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, qd[dg][st], c[dg], 0, 0, 0);
+          }
+          if constexpr (bb > 0) {
+            scores(std::integral_constant<uint32_t, bb - 1>{});
+#pragma unroll
+            for (int i = 0; i < 3 * KS; ++i) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+              __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // then up to three VALU
             }
-          });
-          const bool full = t0 + kTileTokens <= e_min;  // every head-row of the block sees the whole tile
-          const uint32_t vis = e_h > t0 ? (e_h - t0 < kTileTokens ? e_h - t0 : kTileTokens) : 0u;
-          // Masking only on the tiles that need it (separate code paths).
-          auto scores = [&](auto maskc) __attribute__((always_inline)) {
-            constexpr bool MASK = decltype(maskc)::value;
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const int hi2 = cq[0][mb][e] * 256 + cq[1][mb][e];  // |.| < 2^29
-                float s2 = fmaf(float(hi2), 256.f, float(cq[2][mb][e])) * __uint_as_float(ks[mb][e]);
-                if constexpr (MASK) s2 = 16u * g + 4u * mb + e < vis ? s2 : neg_inf();
-                sc[j][4 * mb + e] = s2;
-                mx = fmaxf(mx, s2);
-              }
-            }
-          };
-          if (full) scores(std::false_type{});
-          else scores(std::true_type{});
+          }
         });
+        scores(std::integral_constant<uint32_t, NB - 1>{});
+        };
+        if (phase_full) qk(std::false_type{});
+        else qk(std::true_type{});
+        pin(mx);
 
         // ---- v-scales of the phase, running maximum, weight exponent kp
-        u32x4_t vsr[CT][4];
         float vm = 0.f;
         static_for<0, CT>([&](auto jc) __attribute__((always_inline)) {
           constexpr uint32_t j = decltype(jc)::value;
           constexpr uint32_t TB = j * G::kBufBytes;
           if (tp + j >= nvis) return;
-          ds_read16x4<TB + 256u, TB + 272u, TB + 288u, TB + 304u>(sa, vsr[j][0], vsr[j][1], vsr[j][2], vsr[j][3]);
           const float v = __uint_as_float(ds_read4_sync<TB>(vma));
           const uint32_t t0 = (k_first + tp + j) * kTileTokens;
           vm = t0 + lane < e_max ? fmaxf(vm, fabsf(v)) : vm;
@@ -396,25 +598,28 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
           kp = kp < -100 ? -100 : (kp > 100 ? 100 : kp);
         }
         const float f = m_run == neg_inf() ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-        if (__ballot(f != 1.f) != 0) {
 #pragma unroll
-          for (int mb = 0; mb < MB; ++mb) acc[mb] *= f;
-        }
+        for (int mb = 0; mb < MB; ++mb) acc[mb] *= f;  // exact where f == 1
         const float mu = (m_new == neg_inf() ? 0.f : m_new) - float(kp);  // 2^(s - mu) = w * 2^kp
         m_run = m_new;
 
-        // ---- weights as three 7-bit digits (B of PV), k-position = token 16g + 4mb + e
+        // ---- weights as three 7-bit digits (B of PV), k-position = token 16g + 4mb + e.
+        // Slots past the block's last visible token (and every slot of a tile
+        // past the visible range) get a zero v-scale, so stale LDS contents
+        // cannot reach the digits; the masking is chosen per phase.
         i32x4 bd[CT][3];
         float lw = 0.f;
-        static_for<0, CT>([&](auto jc) __attribute__((always_inline)) {
-          constexpr uint32_t j = decltype(jc)::value;
-          if (tp + j >= nvis) return;
-          const uint32_t t0 = (k_first + tp + j) * kTileTokens;
-          const bool vfull = t0 + kTileTokens <= e_max;  // no token past the block's last visible one
-          const uint32_t vlim = e_max - t0;
-          uint32_t bw[3][4];
-          auto digits = [&](auto maskc) __attribute__((always_inline)) {
-            constexpr bool MASK = decltype(maskc)::value;
+        const bool phase_vfull = tp + CT <= nvis && (k_first + tp + CT) * kTileTokens <= e_max;
+        auto weights = [&](auto maskc) __attribute__((always_inline)) {
+          constexpr bool MASK = decltype(maskc)::value;
+          static_for<0, CT>([&](auto jc) __attribute__((always_inline)) {
+            constexpr uint32_t j = decltype(jc)::value;
+            constexpr uint32_t TB = j * G::kBufBytes;
+            const uint32_t t0 = (k_first + tp + j) * kTileTokens;
+            const uint32_t vlim = tp + j < nvis && e_max > t0 ? (e_max - t0 < kTileTokens ? e_max - t0 : kTileTokens) : 0u;
+            u32x4_t vsr[4];  // v-scales of tokens 16g .. 16g + 15
+            ds_read16x4<TB + 256u, TB + 272u, TB + 288u, TB + 304u>(sa, vsr[0], vsr[1], vsr[2], vsr[3]);
+            uint32_t bw[3][4];
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb) {
               bw[0][mb] = bw[1][mb] = bw[2][mb] = 0u;
@@ -422,8 +627,8 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
               for (int e = 0; e < 4; ++e) {
                 const float w = __builtin_amdgcn_exp2f(fmaf(sc[j][4 * mb + e], cs, -mu));  // w * 2^kp
                 lw += w;
-                float vsl = __uint_as_float(vsr[j][mb][e]);
-                if constexpr (MASK) vsl = 16u * g + 4u * mb + e < vlim ? vsl : 0.f;  // slots past the data
+                float vsl = __uint_as_float(vsr[mb][e]);
+                if constexpr (MASK) vsl = 16u * g + 4u * mb + e < vlim ? vsl : 0.f;
                 // p = w * v_scale rounded to an integer (0 <= p < 2^21) in one fma:
                 // 1.5 * 2^23 + p lies in [2^23, 2^24), where the float's ulp is
                 // 1, so its low 22 bits are p mod 2^22 (two's complement), and
@@ -434,48 +639,83 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
                 bw[2][mb] |= (pb & 0x7fu) << (8 * e);
               }
             }
-          };
-          if (vfull) digits(std::false_type{});
-          else digits(std::true_type{});
 #pragma unroll
-          for (int dg = 0; dg < 3; ++dg)
-            bd[j][dg] = i32x4{int(bw[dg][0]), int(bw[dg][1]), int(bw[dg][2]), int(bw[dg][3])};
-        });
+            for (int dg = 0; dg < 3; ++dg)
+              bd[j][dg] = i32x4{int(bw[dg][0]), int(bw[dg][1]), int(bw[dg][2]), int(bw[dg][3])};
+          });
+        };
+        if (phase_vfull) weights(std::false_type{});
+        else weights(std::true_type{});
         const float inv = __builtin_amdgcn_ldexpf(1.f, -kp);
         l_run = fmaf(lw, inv, l_run * f);
 
-        // ---- PV per 16-dim block: A = V[16mb + n][16g .. 16g + 15], one read per tile
-        static_for<0, MB>([&](auto mc) __attribute__((always_inline)) {
+        // ---- PV per 16-dim block: A = V[16mb + n][16g .. 16g + 15], one read per tile.
+        // Software-pipelined: the reads of block mb + 2 go out while block
+        // mb's MFMAs run (three register sets, so a set is refilled two
+        // blocks after its MFMAs were issued), block mb's MFMAs are
+        // interleaved with block mb - 1's fold into fp32.  Tiles past the
+        // visible range have zero weight digits, so every tile runs without
+        // a branch.
+        u32x4_t vr[3][CT];
+        auto read_v = [&](auto mc) __attribute__((always_inline)) {
           constexpr uint32_t mb = decltype(mc)::value;
-          u32x4_t vr[CT];
+          u32x4_t(&r)[CT] = vr[mb % 3u];
           if constexpr (CT == 2) {
-            ds_read16x2<1024u * mb, G::kBufBytes + 1024u * mb>(va, vr[0], vr[1]);
+            ds_issue16x2<1024u * mb, G::kBufBytes + 1024u * mb>(va, r[0], r[1]);
           } else {
-            ds_read16x4<1024u * mb, G::kBufBytes + 1024u * mb, 2u * G::kBufBytes + 1024u * mb,
-                        3u * G::kBufBytes + 1024u * mb>(va, vr[0], vr[1], vr[2], vr[3]);
+            ds_issue16x4<1024u * mb, G::kBufBytes + 1024u * mb, 2u * G::kBufBytes + 1024u * mb,
+                         3u * G::kBufBytes + 1024u * mb>(va, r[0], r[1], r[2], r[3]);
           }
-          i32x4 cv[3] = {i32x4{0, 0, 0, 0}, i32x4{0, 0, 0, 0}, i32x4{0, 0, 0, 0}};
-          static_for<0, CT>([&](auto jc) __attribute__((always_inline)) {
-            constexpr uint32_t j = decltype(jc)::value;
-            if (tp + j >= nvis) return;
-            const i32x4 av = {int(vr[j][0]), int(vr[j][1]), int(vr[j][2]), int(vr[j][3])};
-#pragma unroll
-            for (int dg = 0; dg < 3; ++dg) cv[dg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bd[j][dg], cv[dg], 0, 0, 0);
-          });
+        };
+        read_v(std::integral_constant<uint32_t, 0>{});
+        if constexpr (MB > 1) read_v(std::integral_constant<uint32_t, 1>{});
+        i32x4 cv[2][3];
+        auto fold = [&](auto mc) __attribute__((always_inline)) {
+          constexpr uint32_t mb = decltype(mc)::value;
+          const i32x4(&c)[3] = cv[mb & 1u];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int hi2 = cv[0][e] * 128 + cv[1][e];  // |.| < 2^29
-            acc[mb][e] = fmaf(fmaf(float(hi2), 128.f, float(cv[2][e])), inv, acc[mb][e]);
+            const int hi2 = c[0][e] * 128 + c[1][e];  // |.| < 2^29
+            acc[mb][e] = fmaf(fmaf(float(hi2), 128.f, float(c[2][e])), inv, acc[mb][e]);
+          }
+        };
+        static_for<0, MB>([&](auto mc) __attribute__((always_inline)) {
+          constexpr uint32_t mb = decltype(mc)::value;
+          // block mb's reads done; block mb + 1's may still be in flight
+          if constexpr (mb + 1 < MB) wait_lgkm<CT>();
+          else wait_lgkm<0>();
+          u32x4_t(&r)[CT] = vr[mb % 3u];
+#pragma unroll
+          for (int j = 0; j < CT; ++j) pin(r[j]);
+          if constexpr (mb + 2 < MB) read_v(std::integral_constant<uint32_t, mb + 2>{});
+          i32x4(&c)[3] = cv[mb & 1u];
+#pragma unroll
+          for (int dg = 0; dg < 3; ++dg) c[dg] = i32x4{0, 0, 0, 0};
+#pragma unroll
+          for (int j = 0; j < CT; ++j) {
+            const i32x4 av = {int(r[j][0]), int(r[j][1]), int(r[j][2]), int(r[j][3])};
+#pragma unroll
+            for (int dg = 0; dg < 3; ++dg) c[dg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bd[j][dg], c[dg], 0, 0, 0);
+          }
+          if constexpr (mb > 0) {
+            fold(std::integral_constant<uint32_t, mb - 1>{});
+            pin(acc[mb - 1]);
+#pragma unroll
+            for (int i = 0; i < 3 * CT; ++i) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+              __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // then up to four VALU
+            }
           }
         });
+        fold(std::integral_constant<uint32_t, MB - 1>{});
+        pin(acc[MB - 1]);
       }
-      if (p + 1u == nphase) write_partial(sp1 - 1u);
-      else if (spw > 1u && (p + 1u) % pps == 0u) write_partial(sp0 + p / pps);
-      __syncthreads();  // slot p & 1 is free
-      if (p + 2u < nphase) issue(p + 2u);
+      if (!idle_dma) {
+        __syncthreads();  // slot p & 1 is free
+        if (p + 2u < nphase) issue(p + 2u);
+      }
     }
-    if (nphase == 0) {  // empty range: empty partials
-      for (uint32_t sp = sp0; sp < sp1; ++sp) write_partial(sp);
+    write_partial(sp);  // (an empty range leaves the empty partial)
     }
   }
 }
