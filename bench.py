@@ -327,9 +327,9 @@ def main():
     log(f"stream probe: {probe_ms*1e3:.2f} us ({gbs(kv_bytes, probe_ms*1e3):.0f} GB/s); paged probe "
         f"{paged_ms*1e3:.2f} us ({gbs(kv_bytes, paged_ms*1e3):.0f} GB/s)")
 
-    # ---- paged INT8 append (kvb_append_kv): a 4096-token prefill chunk
-    # (tokens fill randomly chosen pages in order, as a paged prefill does) and
-    # a one-token decode step into a cfg2-sized pool, fp16 sources.  Gated
+    # ---- paged INT8 append (kvb_append_kv): 4096- and 16384-token prefill
+    # chunks (tokens fill randomly chosen pages in order, as a paged prefill
+    # does) and a one-token decode step into a cfg2-sized pool, fp16 sources.  Gated
     # bitwise against the CPU quantizer; timed as a captured graph of 32
     # appends (device time per append, not Python submission).  Bytes per
     # token and kv head: 2 x dim fp16 read, 2 x dim int8 + 8 B scales written.
@@ -343,7 +343,7 @@ def main():
         avs = torch.zeros((apages, kvh, P), dtype=torch.float32, device=dev)
         gen = torch.Generator(device=dev)
         gen.manual_seed(0x4B56450)
-        for ntok in (4096, 1):
+        for ntok in (4096, 16384, 1):
             kn = torch.randn((ntok, kvh, D), generator=gen, device=dev).half()
             vn = torch.randn((ntok, kvh, D), generator=gen, device=dev).half()
             tok = torch.arange(ntok, device=dev)

@@ -35,6 +35,8 @@
 namespace kvb {
 namespace {
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kWaves = 4;
 constexpr uint32_t kTileMin = 256;  // tokens from which the tile kernel is used
 
@@ -44,10 +46,117 @@ __device__ __forceinline__ float to_f32(T x) {
   else return float(x);
 }
 
+// clamp(rint(x / scale), -127, 127) with x / scale the correctly rounded
+// fp32 quotient, without the IEEE division sequence in the common case.
+// q = x * rcp(scale) is within 1.25 * 2^-22 relative of x / scale
+// (v_rcp_f32 is accurate to 1 ulp, the product adds half an ulp), i.e.
+// within 4e-5 absolute for |q| <= 128, and the correctly rounded quotient is
+// within half an ulp (<= 2^-18) of the exact one.  So wherever q lies more
+// than 2^-13 away from a half-integer, the rounded quotient has the same
+// nearest integer and is no tie: rint(q) is the answer.  The rest (about one
+// element in 4,000, and any non-finite q, e.g. a subnormal scale) take the
+// division.
 __device__ __forceinline__ int8_t quantize(float x, float scale) {
-  float c = __builtin_rintf(x / scale);
+  const float q = x * __builtin_amdgcn_rcpf(scale);
+  float c = __builtin_rintf(q);
+  if (!(fabsf(q - c) <= 0.5f - 0x1p-14f)) c = __builtin_rintf(x / scale);
   c = fminf(fmaxf(c, -127.f), 127.f);
   return int8_t(int(c));
+}
+
+// The codes of N elements of one row (|x| <= absmax, scale = absmax / 127):
+// quantize() for a row slice with the rounding done by one add.  t = x / s
+// + 1.5 * 2^23 lies in [2^23, 2^24), where the fp32 ulp is 1, so the add
+// rounds to the nearest integer (ties to even: rint) and t's low byte is the
+// code; |x / s| <= 127.00001, so no clamp is needed.  A lane with any element
+// near a half-integer recomputes its slice with the division.
+constexpr float kRoundMagic = 12582912.f;  // 1.5 * 2^23
+template <uint32_t N>
+__device__ __forceinline__ void quantize_slice(const float (&x)[N], float scale, uint32_t (&t)[N]) {
+  const float r = __builtin_amdgcn_rcpf(scale);
+  uint32_t amb = 0u;
+#pragma unroll
+  for (uint32_t e = 0; e < N; ++e) {
+    const float q = x[e] * r;
+    const float ti = q + kRoundMagic;
+    amb |= fabsf(q - (ti - kRoundMagic)) <= 0.5f - 0x1p-14f ? 0u : 1u;  // NaN counts as near
+    t[e] = __float_as_uint(ti);
+  }
+  if (amb != 0u) {  // rare: one branch per slice
+#pragma unroll
+    for (uint32_t e = 0; e < N; ++e) t[e] = __float_as_uint(x[e] / scale + kRoundMagic);
+  }
+}
+
+// |x| max of the N elements of type T in a 16-byte word (exact: max picks
+// an element).  fp16: the sign bits cleared, finite halves order like their
+// 16-bit patterns, so a packed unsigned 16-bit max (two elements an
+// instruction) finds the largest magnitude.
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+template <class T, uint32_t N>
+__device__ __forceinline__ float word_absmax(const u32x4& w) {
+  if constexpr (std::is_same<T, _Float16>::value) {
+    u16x2 m = __builtin_bit_cast(u16x2, w[0] & 0x7fff7fffu);
+#pragma unroll
+    for (int j = 1; j < 4; ++j) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[j] & 0x7fff7fffu));
+    const uint16_t b = m[0] > m[1] ? m[0] : m[1];
+    return float(__builtin_bit_cast(_Float16, b));
+  } else {
+    const T* e = reinterpret_cast<const T*>(&w);
+    float a = 0.f;
+#pragma unroll
+    for (uint32_t i = 0; i < N; ++i) a = fmaxf(a, fabsf(to_f32(e[i])));
+    return a;
+  }
+}
+
+// quantize_slice on the N elements of a 16-byte word: the product with the
+// reciprocal, the rounding add and the check in mixed-precision fmas (fp16
+// elements need no conversion instruction).  t = RN(x * r + 1.5 * 2^23)
+// rounds the exact product x * r to the nearest integer n directly, and
+// d = RN(x * r - n) measures its distance from n; the same 2^-14 margin as
+// quantize() applies (|x * r - x / scale| <= 4e-5).
+template <class T, uint32_t N>
+__device__ __forceinline__ void quantize_word(const u32x4& w, float scale, uint32_t (&t)[N]) {
+  const T* e = reinterpret_cast<const T*>(&w);
+  const float r = __builtin_amdgcn_rcpf(scale);
+  uint32_t amb = 0u;
+#pragma unroll
+  for (uint32_t i = 0; i < N; ++i) {
+    const float x = to_f32(e[i]);
+    const float ti = fmaf(x, r, kRoundMagic);
+    const float d = fmaf(x, r, -(ti - kRoundMagic));
+    amb |= fabsf(d) <= 0.5f - 0x1p-14f ? 0u : 1u;  // NaN counts as near
+    t[i] = __float_as_uint(ti);
+  }
+  if (amb != 0u) {  // rare: one branch per word
+#pragma unroll
+    for (uint32_t i = 0; i < N; ++i) t[i] = __float_as_uint(to_f32(e[i]) / scale + kRoundMagic);
+  }
+}
+
+// Max over aligned groups of L lanes (L a power of two, 4..64), in every lane
+// of the group: DPP quad permutes and row mirrors inside a 16-lane row, then
+// the gfx950 permlane swaps across rows.
+template <uint32_t L>
+__device__ __forceinline__ float group_max(float x) {
+  static_assert(L >= 4 && L <= 64 && (L & (L - 1)) == 0, "group size");
+  auto dpp = [](float v, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), decltype(ctrl)::value, 0xF, 0xF, false));
+  };
+  x = fmaxf(x, dpp(x, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
+  x = fmaxf(x, dpp(x, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
+  if constexpr (L >= 8) x = fmaxf(x, dpp(x, std::integral_constant<int, 0x141>{}));  // row_half_mirror
+  if constexpr (L >= 16) x = fmaxf(x, dpp(x, std::integral_constant<int, 0x140>{}));  // row_mirror
+  if constexpr (L >= 32) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
+    x = fmaxf(__int_as_float(p[0]), __int_as_float(p[1]));
+  }
+  if constexpr (L >= 64) {
+    auto p = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    x = fmaxf(__int_as_float(p[0]), __int_as_float(p[1]));
+  }
+  return x;
 }
 
 template <class T>
@@ -99,8 +208,6 @@ __global__ __launch_bounds__(64 * kWaves) void append_row_kernel(AppendArgs a) {
     a.v_scales[row] = vs;
   }
 }
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // 16 consecutive source elements of a row as floats (VEC: 16-byte loads).
 template <class T, bool VEC>
@@ -199,7 +306,7 @@ __global__ __launch_bounds__(64 * kWaves) void append_tile_kernel(AppendArgs a) 
 // LDS ([dim][64 tokens]) and stored 16 tokens per 16-byte store where those
 // 16 tokens fill 16 consecutive slots of one page starting on a 16-slot
 // boundary (a prefill chunk); any other group of 16 is stored byte by byte.
-template <class T, int D>
+template <class T, int D, bool P2>  // P2: page_tokens is a power of two
 __global__ __launch_bounds__(64 * kWaves) void append_stream_kernel(AppendArgs a) {
   constexpr uint32_t EPL = 16 / sizeof(T);  // elements per lane per load
   constexpr uint32_t LPR = D / EPL;         // lanes per row
@@ -209,8 +316,28 @@ __global__ __launch_bounds__(64 * kWaves) void append_stream_kernel(AppendArgs a
   __shared__ uint32_t ids[64];
   __shared__ uint32_t grp_ok[4];
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-  const uint32_t kv = blockIdx.y, t0 = blockIdx.x * 64u;
+  const uint32_t kv = blockIdx.x, t0 = blockIdx.y * 64u;  // the kv heads of a tile are consecutive work-groups
   const uint32_t P = a.page_tokens, cap = a.pages * a.page_tokens;
+  const uint32_t psh = __builtin_ctz(P);
+  auto page_of = [&](uint32_t id) { return P2 ? id >> psh : id / P; };
+  auto slot_of = [&](uint32_t id) { return P2 ? id & (P - 1u) : id % P; };
+  constexpr uint32_t NI = 16u / RPL;  // row slices per lane
+  const uint32_t sub = lane % LPR, e0 = sub * EPL;
+  // Every source load of the wave first (they do not depend on the slot
+  // ids), so they are all in flight together; then the slot ids.
+  u32x4 wk[NI], wv[NI];
+#pragma unroll
+  for (uint32_t i = 0; i < NI; ++i) {
+    const uint32_t t = t0 + 16u * wave + RPL * i + lane / LPR;
+    if (t < a.tokens) {
+      wk[i] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k_new) + size_t(t) * a.k_stride +
+                                              size_t(kv) * D + e0);
+      wv[i] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v_new) + size_t(t) * a.v_stride +
+                                              size_t(kv) * D + e0);
+    } else {
+      wk[i] = wv[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
   if (wave == 0) {
     const uint32_t t = t0 + lane;
     const uint32_t id = t < a.tokens ? a.slots[t] : cap;
@@ -221,53 +348,26 @@ __global__ __launch_bounds__(64 * kWaves) void append_stream_kernel(AppendArgs a
     if ((lane & 15u) == 0u) grp_ok[lane >> 4] = ((b >> (lane & ~15u)) & 0xffffull) == 0xffffull ? 1u : 0u;
   }
   __syncthreads();
-  const uint32_t sub = lane % LPR, e0 = sub * EPL;
 #pragma unroll
-  for (uint32_t i = 0; i < 16u / RPL; ++i) {
+  for (uint32_t i = 0; i < NI; ++i) {
     const uint32_t r = 16u * wave + RPL * i + lane / LPR;  // token of the tile
-    const uint32_t t = t0 + r;
     const uint32_t id = ids[r];
-    const bool live = t < a.tokens;
-    float xk[EPL], xv[EPL];
-    if (live) {  // one 16-byte load of each row slice
-      const u32x4 wk = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k_new) + size_t(t) * a.k_stride +
-                                                       size_t(kv) * D + e0);
-      const u32x4 wv = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v_new) + size_t(t) * a.v_stride +
-                                                       size_t(kv) * D + e0);
-      const T* ek = reinterpret_cast<const T*>(&wk);
-      const T* ev = reinterpret_cast<const T*>(&wv);
-#pragma unroll
-      for (uint32_t e = 0; e < EPL; ++e) {
-        xk[e] = to_f32(ek[e]);
-        xv[e] = to_f32(ev[e]);
-      }
-    } else {
-#pragma unroll
-      for (uint32_t e = 0; e < EPL; ++e) xk[e] = xv[e] = 0.f;
-    }
-    float ka = 0.f, va = 0.f;
-#pragma unroll
-    for (uint32_t e = 0; e < EPL; ++e) {
-      ka = fmaxf(ka, fabsf(xk[e]));
-      va = fmaxf(va, fabsf(xv[e]));
-    }
-#pragma unroll
-    for (uint32_t o = 1; o < LPR; o <<= 1) {
-      ka = fmaxf(ka, __shfl_xor(ka, int(o)));
-      va = fmaxf(va, __shfl_xor(va, int(o)));
-    }
+    const float ka = group_max<LPR>(word_absmax<T, EPL>(wk[i]));  // the row's lanes are an aligned group
+    const float va = group_max<LPR>(word_absmax<T, EPL>(wv[i]));
     const float ks = ka == 0.f ? 1.f : ka / 127.f;
     const float vs = va == 0.f ? 1.f : va / 127.f;
+    uint32_t tk[EPL], tv[EPL];
+    quantize_word<T, EPL>(wk[i], ks, tk);
+    quantize_word<T, EPL>(wv[i], vs, tv);
     uint32_t kw[EPL / 4];
 #pragma unroll
-    for (uint32_t e = 0; e < EPL / 4; ++e) kw[e] = 0u;
+    for (uint32_t e = 0; e < EPL / 4; ++e)  // low bytes of four words
+      kw[e] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(tk[4 * e + 3], tk[4 * e + 2], 0x0c0c0400u),
+                                    __builtin_amdgcn_perm(tk[4 * e + 1], tk[4 * e], 0x0c0c0400u), 0x05040100u);
 #pragma unroll
-    for (uint32_t e = 0; e < EPL; ++e) {
-      kw[e / 4] |= uint32_t(uint8_t(quantize(xk[e], ks))) << (8 * (e % 4));
-      vt[(e0 + e) * 64u + r] = uint8_t(quantize(xv[e], vs));
-    }
+    for (uint32_t e = 0; e < EPL; ++e) vt[(e0 + e) * 64u + r] = uint8_t(tv[e]);
     if (id < cap) {
-      const size_t row = (size_t(id / P) * a.kv_heads + kv) * P + id % P;
+      const size_t row = (size_t(page_of(id)) * a.kv_heads + kv) * P + slot_of(id);
       int8_t* const kdst = a.k + row * D + e0;
       if constexpr (EPL == 8) *reinterpret_cast<uint2*>(kdst) = uint2{kw[0], kw[1]};
       else *reinterpret_cast<uint32_t*>(kdst) = kw[0];
@@ -284,13 +384,13 @@ __global__ __launch_bounds__(64 * kWaves) void append_stream_kernel(AppendArgs a
     const uint8_t* const src = vt + d * 64u + 16u * q;
     if (grp_ok[q]) {
       const uint32_t id = ids[16u * q];
-      int8_t* const dst = a.v + (size_t(id / P) * a.kv_heads + kv) * D * P + size_t(d) * P + id % P;
+      int8_t* const dst = a.v + (size_t(page_of(id)) * a.kv_heads + kv) * D * P + size_t(d) * P + slot_of(id);
       *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
     } else {
 #pragma unroll 4
       for (uint32_t j = 0; j < 16u; ++j) {
         const uint32_t id = ids[16u * q + j];
-        if (id < cap) a.v[(size_t(id / P) * a.kv_heads + kv) * D * P + size_t(d) * P + id % P] = int8_t(src[j]);
+        if (id < cap) a.v[(size_t(page_of(id)) * a.kv_heads + kv) * D * P + size_t(d) * P + slot_of(id)] = int8_t(src[j]);
       }
     }
   }
@@ -311,18 +411,19 @@ hipError_t launch_typed(const AppendArgs& a, hipStream_t stream) {
   const dim3 grid((a.tokens + 63u) / 64u, a.kv_heads);
   // Row-streaming kernel: 16-byte aligned sources and strides, aligned K and V
   // pools, whole 16-slot groups in a page.
-  const bool stream_ok = vec && reinterpret_cast<uintptr_t>(a.v) % 16 == 0 && a.page_tokens % 16 == 0;
-  if (stream_ok && a.dim == 64) {
-    hipLaunchKernelGGL((append_stream_kernel<T, 64>), grid, dim3(64 * kWaves), 0, stream, a);
-    return hipGetLastError();
-  }
-  if (stream_ok && a.dim == 128) {
-    hipLaunchKernelGGL((append_stream_kernel<T, 128>), grid, dim3(64 * kWaves), 0, stream, a);
-    return hipGetLastError();
-  }
-  if (stream_ok && a.dim == 256) {
-    hipLaunchKernelGGL((append_stream_kernel<T, 256>), grid, dim3(64 * kWaves), 0, stream, a);
-    return hipGetLastError();
+  const bool stream_ok = vec && reinterpret_cast<uintptr_t>(a.v) % 16 == 0 && a.page_tokens % 16 == 0 &&
+                         (a.tokens + 63u) / 64u <= 65535u;  // tiles on grid.y
+  const dim3 sgrid(a.kv_heads, (a.tokens + 63u) / 64u);
+  if (stream_ok) {
+    const bool p2 = (a.page_tokens & (a.page_tokens - 1u)) == 0u;
+    auto go = [&](auto dc) {
+      constexpr int DD = decltype(dc)::value;
+      if (p2) hipLaunchKernelGGL((append_stream_kernel<T, DD, true>), sgrid, dim3(64 * kWaves), 0, stream, a);
+      else hipLaunchKernelGGL((append_stream_kernel<T, DD, false>), sgrid, dim3(64 * kWaves), 0, stream, a);
+    };
+    if (a.dim == 64) { go(std::integral_constant<int, 64>{}); return hipGetLastError(); }
+    if (a.dim == 128) { go(std::integral_constant<int, 128>{}); return hipGetLastError(); }
+    if (a.dim == 256) { go(std::integral_constant<int, 256>{}); return hipGetLastError(); }
   }
   if (vec) hipLaunchKernelGGL((append_tile_kernel<T, true>), grid, dim3(64 * kWaves), 0, stream, a);
   else hipLaunchKernelGGL((append_tile_kernel<T, false>), grid, dim3(64 * kWaves), 0, stream, a);
@@ -351,15 +452,24 @@ hipError_t preload_append() {
                        reinterpret_cast<const void*>(&append_tile_kernel<_Float16, false>),
                        reinterpret_cast<const void*>(&append_tile_kernel<__bf16, true>),
                        reinterpret_cast<const void*>(&append_tile_kernel<__bf16, false>),
-                       reinterpret_cast<const void*>(&append_stream_kernel<float, 64>),
-                       reinterpret_cast<const void*>(&append_stream_kernel<float, 128>),
-                       reinterpret_cast<const void*>(&append_stream_kernel<float, 256>),
-                       reinterpret_cast<const void*>(&append_stream_kernel<_Float16, 64>),
-                       reinterpret_cast<const void*>(&append_stream_kernel<_Float16, 128>),
-                       reinterpret_cast<const void*>(&append_stream_kernel<_Float16, 256>),
-                       reinterpret_cast<const void*>(&append_stream_kernel<__bf16, 64>),
-                       reinterpret_cast<const void*>(&append_stream_kernel<__bf16, 128>),
-                       reinterpret_cast<const void*>(&append_stream_kernel<__bf16, 256>)};
+                       reinterpret_cast<const void*>(&append_stream_kernel<float, 64, true>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<float, 64, false>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<float, 128, true>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<float, 128, false>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<float, 256, true>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<float, 256, false>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<_Float16, 64, true>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<_Float16, 64, false>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<_Float16, 128, true>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<_Float16, 128, false>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<_Float16, 256, true>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<_Float16, 256, false>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<__bf16, 64, true>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<__bf16, 64, false>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<__bf16, 128, true>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<__bf16, 128, false>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<__bf16, 256, true>),
+                       reinterpret_cast<const void*>(&append_stream_kernel<__bf16, 256, false>)};
   hipFuncAttributes attr{};
   for (const void* f : fns) {
     const hipError_t e = hipFuncGetAttributes(&attr, f);

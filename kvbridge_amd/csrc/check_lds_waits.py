@@ -7,7 +7,8 @@ the compiler's own wait insertion).  Were such a read's wait emitted later
 than the read, the compiler could copy or reuse its destination before the
 data lands -- silent garbage.  LDS-counter (lgkmcnt) operations complete in
 issue order for this purpose, so s_waitcnt lgkmcnt(N) retires all but the N
-most recent pending operations; scalar memory loads and ds_bpermute count too.
+most recent pending operations; every DS operation (LDS writes included),
+scalar memory loads and messages count too.
 
 Usage: python check_lds_waits.py FILE.s ...   (exit status 1 on findings)
 The assembly comes from `make -C kvbridge_amd/csrc asm` (the build's flags).
@@ -15,7 +16,7 @@ The assembly comes from `make -C kvbridge_amd/csrc asm` (the build's flags).
 import re
 import sys
 
-_LGKM = re.compile(r"^(ds_read\w*|ds_bpermute\w*|ds_permute\w*|ds_swizzle\w*|s_load\w*|s_buffer_load\w*)\s")
+_LGKM = re.compile(r"^(ds_\w+|s_load\w*|s_buffer_load\w*|s_sendmsg\w*)\s")  # every op the LDS counter counts
 _VDST = re.compile(r"^\S+\s+(?:v\[(\d+):(\d+)\]|v(\d+))")
 _VREG = re.compile(r"v\[(\d+):(\d+)\]|(?<![a-z_])v(\d+)")
 _WAIT = re.compile(r"lgkmcnt\((\d+)\)")

@@ -107,6 +107,59 @@ def test_append_prefill_mapping_matches_oracle_bitwise(gpu, case):
     _run_append(gpu, tokens, kvh, D, P, src, 0, slots, pages, seed=tokens * 7 + D)
 
 
+NEAR_TIE_CASES = [
+    # tokens, kv_heads, dim, page, src: the row, tile and row-streaming kernels
+    (3, 4, 128, 64, kvb.KVB_SRC_F32),
+    (300, 4, 67, 32, kvb.KVB_SRC_F32),
+    (320, 4, 128, 64, kvb.KVB_SRC_F32),
+    (320, 4, 128, 64, kvb.KVB_SRC_F16),
+]
+
+
+@pytest.mark.parametrize("case", NEAR_TIE_CASES)
+def test_append_near_ties_matches_oracle_bitwise(gpu, case):
+    """Elements whose quotient x / scale lies within a few ulp of a
+    half-integer (or exactly on one), where the kernels' reciprocal fast path
+    must defer to the correctly rounded division: codes bitwise the CPU
+    quantizer's (rint of the fp32 quotient, ties to even)."""
+    import torch
+
+    tokens, kvh, D, P, src = case
+    rng = np.random.default_rng(tokens * 13 + D + src)
+    pages = -(-tokens // P) + 1
+    slots = rng.permutation(pages * P)[:tokens].astype(np.uint32)
+    tdt = getattr(torch, SRC[src])
+    bufs = []
+    for _ in range(2):
+        amax = (rng.random((tokens, kvh, 1)) * 4 + 0.25).astype(np.float32)
+        amax = torch.from_numpy(amax).to(tdt).float().numpy()     # representable in the source type
+        scale = (amax / np.float32(127)).astype(np.float32)
+        k = rng.integers(-127, 127, (tokens, kvh, D)).astype(np.float32) + np.float32(0.5)
+        x = (k * scale).astype(np.float32)                         # at or next to a tie
+        steps = rng.integers(-3, 4, (tokens, kvh, D))
+        for _s in range(3):                                        # move up to 3 ulp either way
+            x = np.where(steps > _s, np.nextafter(x, np.float32(np.inf)), x)
+            x = np.where(-steps > _s, np.nextafter(x, np.float32(-np.inf)), x)
+        x = np.clip(x, -amax, amax)
+        x[..., 0] = amax[..., 0]                                   # the row's absmax itself
+        xt = torch.from_numpy(x.astype(np.float32)).to(tdt)        # fp16 sources round to near-ties of their own
+        bufs.append(xt.reshape(tokens, kvh * D))
+    kbuf, vbuf = bufs
+    pool = random_pool(pages, kvh, P, D, seed=tokens)
+    kn = kbuf.float().numpy().reshape(tokens, kvh, D)
+    vn = vbuf.float().numpy().reshape(tokens, kvh, D)
+    want = O.append_int8(*pool, kn, vn, slots, P)
+    dev = [torch.from_numpy(np.ascontiguousarray(a)).to(gpu) for a in pool]
+    s = kvb.append_shape(tokens, kvh, D, P, pages, src)
+    log(f"near-tie append tokens={tokens} kv={kvh} dim={D} page={P} src={SRC[src]}")
+    kvb.append_kv(s, kbuf.to(gpu), vbuf.to(gpu), torch.from_numpy(slots.view(np.int32)).to(gpu), *dev)
+    torch.cuda.synchronize()
+    for name, g, w in zip(("k", "v", "k_scales", "v_scales"), dev, want):
+        got = g.cpu().numpy()
+        assert np.array_equal(got.view(np.uint8) if got.dtype == np.int8 else got.view(np.uint32),
+                              w.view(np.uint8) if w.dtype == np.int8 else w.view(np.uint32)), f"{name} differs"
+
+
 def test_cache_written_by_append_decodes(gpu):
     """Prefill a cfg2-shaped (shorter) cache through three append calls; it
     equals the synthetic generator's cache bitwise and decodes to FP64."""
