@@ -18,6 +18,11 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 constexpr uint32_t kTileTokens = 64;
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
+// Cache policy of every K/V/scale DMA load: non-temporal (each byte is read
+// once per call).  At the dense rows-8 / group-6 / dim-256 geometry the
+// 1,024-token split kernel measured 43.25 against 43.9 us with cached loads.
+constexpr int kDmaAux = 2;
+
 template <int D>
 struct Geo {
   static constexpr uint32_t kChunks = D / 16;                 // 16-byte chunks per K row
@@ -130,7 +135,7 @@ __device__ __forceinline__ void issue_tile(const Ctx& c, uint32_t tile, uint8_t*
     const uint32_t slot = (t0 + 16u * grp) % c.P + (r & 15u);
     const uint32_t row = (pick4(pg, grp) * c.kv_heads + c.kv) * c.P + slot;
     const int8_t* src = c.k + size_t(row) * D + 16u * chunk;
-    __builtin_amdgcn_global_load_lds(src, (lds_ptr)(buf + 1024u * i), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(src, (lds_ptr)(buf + 1024u * i), 16, 0, kDmaAux);
   }
   // V: load i covers dim rows [16i, 16i+16), 4 chunks (token groups) per row.
   uint8_t* vb = buf + G::kKBytes;
@@ -140,15 +145,15 @@ __device__ __forceinline__ void issue_tile(const Ctx& c, uint32_t tile, uint8_t*
     const uint32_t grp = (lane & 3u) ^ swz_v(d);
     const uint32_t slab = pick4(pg, grp) * c.kv_heads + c.kv;
     const int8_t* src = c.v + (size_t(slab) * D + d) * c.P + (t0 + 16u * grp) % c.P;
-    __builtin_amdgcn_global_load_lds(src, (lds_ptr)(vb + 1024u * i), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(src, (lds_ptr)(vb + 1024u * i), 16, 0, kDmaAux);
   }
   // Scales of token t0 + lane.
   {
     const uint32_t grp = lane >> 4;
     const uint32_t si = (pick4(pg, grp) * c.kv_heads + c.kv) * c.P + (t0 + 16u * grp) % c.P + (lane & 15u);
     uint8_t* sb = buf + G::kKBytes + G::kVBytes;
-    __builtin_amdgcn_global_load_lds(c.ks + si, (lds_ptr)(sb), 4, 0, 0);
-    __builtin_amdgcn_global_load_lds(c.vs + si, (lds_ptr)(sb + 256), 4, 0, 0);
+    __builtin_amdgcn_global_load_lds(c.ks + si, (lds_ptr)(sb), 4, 0, kDmaAux);
+    __builtin_amdgcn_global_load_lds(c.vs + si, (lds_ptr)(sb + 256), 4, 0, kDmaAux);
   }
 }
 
@@ -194,17 +199,17 @@ __device__ __forceinline__ void pt_issue(const PtCtx& c, uint32_t slab, uint32_t
 #pragma unroll
   for (uint32_t i = 0; i < G::kChunks; ++i)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rk, (lds_ptr)(buf + 1024u * i), 16,
-                                             i < 8 ? c.voff_k[i] : c.voff_k2[i - 8], kbase, 0, 0);
+                                             i < 8 ? c.voff_k[i] : c.voff_k2[i - 8], kbase, 0, kDmaAux);
   const uint32_t vbase = slab * D * P + slot0;  // V row 0 of the tile
   uint8_t* vb = buf + G::kKBytes;
 #pragma unroll
   for (uint32_t i = 0; i < D / 16; ++i)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rv, (lds_ptr)(vb + 1024u * i), 16, c.voff_v,
-                                             vbase + 16u * i * P, 0, 0);
+                                             vbase + 16u * i * P, 0, kDmaAux);
   const uint32_t sbase = (slab * P + slot0) * 4u;
   uint8_t* sb = buf + G::kKBytes + G::kVBytes;
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rks, (lds_ptr)(sb), 4, c.voff_s, sbase, 0, 0);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rvs, (lds_ptr)(sb + 256), 4, c.voff_s, sbase, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rks, (lds_ptr)(sb), 4, c.voff_s, sbase, 0, kDmaAux);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rvs, (lds_ptr)(sb + 256), 4, c.voff_s, sbase, 0, kDmaAux);
 }
 
 // ---- one tile's DMA shared by WT waves: wave `part` issues the K and V
@@ -251,19 +256,19 @@ __device__ __forceinline__ void pt_part_issue(const PtPart<D, WT>& c, uint32_t s
 #pragma unroll
   for (uint32_t m = 0; m < PtPart<D, WT>::kK; ++m)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rk, (lds_ptr)(buf + 1024u * (part + WT * m)), 16, c.voff_k[m], kbase,
-                                             0, 0);
+                                             0, kDmaAux);
   const uint32_t vbase = slab * D * P + slot0;
   uint8_t* vb = buf + G::kKBytes;
 #pragma unroll
   for (uint32_t m = 0; m < PtPart<D, WT>::kV; ++m) {
     const uint32_t i = part + WT * m;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rv, (lds_ptr)(vb + 1024u * i), 16, c.voff_v, vbase + 16u * i * P, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rv, (lds_ptr)(vb + 1024u * i), 16, c.voff_v, vbase + 16u * i * P, 0, kDmaAux);
   }
   uint8_t* sb = buf + G::kKBytes + G::kVBytes;
   if (WT == 1u || part == 0u)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rks, (lds_ptr)(sb), 4, c.voff_s, (slab * P + slot0) * 4u, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rks, (lds_ptr)(sb), 4, c.voff_s, (slab * P + slot0) * 4u, 0, kDmaAux);
   if (WT == 1u || part == 1u)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rvs, (lds_ptr)(sb + 256), 4, c.voff_s, (slab * P + slot0) * 4u, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rvs, (lds_ptr)(sb + 256), 4, c.voff_s, (slab * P + slot0) * 4u, 0, kDmaAux);
 }
 
 // Any page size: this wave's share of tile `tile` (pages of its four
@@ -281,7 +286,7 @@ __device__ __forceinline__ void part_issue(const Ctx& c, uint32_t tile, uint8_t*
     const uint32_t chunk = (lane % G::kChunks) ^ swz_k<D>(r);
     const uint32_t grp = r >> 4;
     const uint32_t row = (pick4(pg, grp) * c.kv_heads + c.kv) * c.P + (t0 + 16u * grp) % c.P + (r & 15u);
-    __builtin_amdgcn_global_load_lds(c.k + size_t(row) * D + 16u * chunk, (lds_ptr)(buf + 1024u * i), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(c.k + size_t(row) * D + 16u * chunk, (lds_ptr)(buf + 1024u * i), 16, 0, kDmaAux);
   }
   uint8_t* vb = buf + G::kKBytes;
 #pragma unroll
@@ -291,14 +296,14 @@ __device__ __forceinline__ void part_issue(const Ctx& c, uint32_t tile, uint8_t*
     const uint32_t grp = (lane & 3u) ^ swz_v(d);
     const uint32_t slab = pick4(pg, grp) * c.kv_heads + c.kv;
     __builtin_amdgcn_global_load_lds(c.v + (size_t(slab) * D + d) * c.P + (t0 + 16u * grp) % c.P,
-                                     (lds_ptr)(vb + 1024u * i), 16, 0, 0);
+                                     (lds_ptr)(vb + 1024u * i), 16, 0, kDmaAux);
   }
   if (WT == 1u || part < 2u) {
     const uint32_t grp = lane >> 4;
     const uint32_t si = (pick4(pg, grp) * c.kv_heads + c.kv) * c.P + (t0 + 16u * grp) % c.P + (lane & 15u);
     uint8_t* sb = buf + G::kKBytes + G::kVBytes;
-    if (WT == 1u || part == 0u) __builtin_amdgcn_global_load_lds(c.ks + si, (lds_ptr)(sb), 4, 0, 0);
-    if (WT == 1u || part == 1u) __builtin_amdgcn_global_load_lds(c.vs + si, (lds_ptr)(sb + 256), 4, 0, 0);
+    if (WT == 1u || part == 0u) __builtin_amdgcn_global_load_lds(c.ks + si, (lds_ptr)(sb), 4, 0, kDmaAux);
+    if (WT == 1u || part == 1u) __builtin_amdgcn_global_load_lds(c.vs + si, (lds_ptr)(sb + 256), 4, 0, kDmaAux);
   }
 }
 
@@ -347,18 +352,18 @@ __device__ __forceinline__ void pt_issue_item(const PtCtx& c, bool is_v, uint32_
 #pragma unroll
     for (uint32_t i = 0; i < G::kChunks; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rk, (lds_ptr)(buf + 1024u * i), 16,
-                                               i < 8 ? c.voff_k[i] : c.voff_k2[i - 8], kbase, 0, 0);
+                                               i < 8 ? c.voff_k[i] : c.voff_k2[i - 8], kbase, 0, kDmaAux);
   } else {
     const uint32_t vbase = slab * D * P + slot0;
 #pragma unroll
     for (uint32_t i = 0; i < D / 16; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rv, (lds_ptr)(buf + 1024u * i), 16, c.voff_v,
-                                               vbase + 16u * i * P, 0, 0);
+                                               vbase + 16u * i * P, 0, kDmaAux);
   }
   const uint32_t sbase = (slab * P + slot0) * 4u;
   uint8_t* sb = buf + G::kKBytes;
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rks, (lds_ptr)(sb), 4, c.voff_s, sbase, 0, 0);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rvs, (lds_ptr)(sb + 256), 4, c.voff_s, sbase, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rks, (lds_ptr)(sb), 4, c.voff_s, sbase, 0, kDmaAux);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rvs, (lds_ptr)(sb + 256), 4, c.voff_s, sbase, 0, kDmaAux);
 }
 
 template <int D>
@@ -375,7 +380,7 @@ __device__ __forceinline__ void gen_issue_item(const Ctx& c, bool is_v, uint32_t
       const uint32_t grp = r >> 4;
       const uint32_t slot = (t0 + 16u * grp) % c.P + (r & 15u);
       const uint32_t row = (pick4(pg, grp) * c.kv_heads + c.kv) * c.P + slot;
-      __builtin_amdgcn_global_load_lds(c.k + size_t(row) * D + 16u * chunk, (lds_ptr)(buf + 1024u * i), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(c.k + size_t(row) * D + 16u * chunk, (lds_ptr)(buf + 1024u * i), 16, 0, kDmaAux);
     }
   } else {
 #pragma unroll
@@ -384,14 +389,14 @@ __device__ __forceinline__ void gen_issue_item(const Ctx& c, bool is_v, uint32_t
       const uint32_t grp = (lane & 3u) ^ swz_v(d);
       const uint32_t slab = pick4(pg, grp) * c.kv_heads + c.kv;
       __builtin_amdgcn_global_load_lds(c.v + (size_t(slab) * D + d) * c.P + (t0 + 16u * grp) % c.P,
-                                       (lds_ptr)(buf + 1024u * i), 16, 0, 0);
+                                       (lds_ptr)(buf + 1024u * i), 16, 0, kDmaAux);
     }
   }
   const uint32_t grp = lane >> 4;
   const uint32_t si = (pick4(pg, grp) * c.kv_heads + c.kv) * c.P + (t0 + 16u * grp) % c.P + (lane & 15u);
   uint8_t* sb = buf + G::kKBytes;
-  __builtin_amdgcn_global_load_lds(c.ks + si, (lds_ptr)(sb), 4, 0, 0);
-  __builtin_amdgcn_global_load_lds(c.vs + si, (lds_ptr)(sb + 256), 4, 0, 0);
+  __builtin_amdgcn_global_load_lds(c.ks + si, (lds_ptr)(sb), 4, 0, kDmaAux);
+  __builtin_amdgcn_global_load_lds(c.vs + si, (lds_ptr)(sb + 256), 4, 0, kDmaAux);
 }
 
 __device__ __forceinline__ uint32_t ds_read4(uint32_t addr) {
