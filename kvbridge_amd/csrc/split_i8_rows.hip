@@ -167,6 +167,10 @@ __device__ __forceinline__ void ds_issue_kblock(const uint32_t (&a)[2], uint32_t
       : "v"(a[0]), "v"(a[1]), "v"(as), "i"(OK), "i"(OS)
       : "memory");
 }
+template <uint32_t O0>
+__device__ __forceinline__ void ds_issue16x1(uint32_t a, u32x4_t& r0) {
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(r0) : "v"(a), "i"(O0) : "memory");
+}
 template <uint32_t N>
 __device__ __forceinline__ void wait_lgkm() { asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory"); }
 
@@ -720,6 +724,502 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
   }
 }
 
+// ---- Wave-specialized form: one round of at most three head-row blocks at
+// dim 256 (the dense rows-8 / group-6 geometry, 48 head-rows).
+//
+// Eight waves per work-group: QK waves 0-2 (head-row block b = wave), the DMA
+// wave 3, and PV waves 4-7.  The four-wave kernel above runs one wave per
+// SIMD, and only three of them compute at 48 head-rows; a wave then stalls
+// on every dependent MFMA -> VALU -> LDS step of its own.  Here each block's
+// scores and weights run on a QK wave, and the PV products and fp32 folds of
+// all blocks are spread over four PV waves (wave 4 + j takes dims 64j ..
+// 64j + 63 of every block, whose V rows it reads once for all blocks), so
+// every SIMD computes and each holds two waves that fill each other's
+// stalls (waves w and w + 4 share a SIMD).  Step s (one 64-token tile; the
+// split's tiles run through a four-slot ring of tile images):
+//  - DMA: tile s landed (the wave's loads in flight are tiles s and s + 1),
+//    barrier, then tile s + 2 goes into slot (s + 2) % 4 (two tiles of lead;
+//    that slot held tile s - 2, whose last reader, PV step s - 1, is behind
+//    the barrier);
+//  - QK wave: scores of tile s, running maximum, the weights' three 7-bit
+//    digits (B of PV) into its exchange slot s & 1 with the rescale factor f
+//    of each head-row and 2^-kp;
+//  - PV waves: tile s - 1 from the other exchange slots, acc = acc * f +
+//    (V . P) * 2^-kp per block.
+// One barrier per step.  The arithmetic is the four-wave kernel's per
+// 64-token step instead of per 128-token phase (running maximum, kp and the
+// digit fold per tile), so the partials agree with it to rounding.  The QK
+// wave owns m and l of its block's head-rows and the PV waves the
+// numerators; each writes its part of a split's partial after the split's
+// last tile.
+constexpr uint32_t kPcBlocks = 3;
+constexpr uint32_t kPcWaves = 8;
+constexpr uint32_t kPcSlots = 4;
+
+template <int D, bool PT>
+__global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
+    SplitArgs a, const float* __restrict__ q, const int64_t* __restrict__ qpos,
+    const int64_t* __restrict__ kpos, const uint32_t* __restrict__ table,
+    const int8_t* __restrict__ kdata, const int8_t* __restrict__ vdata,
+    const float* __restrict__ kscale, const float* __restrict__ vscale, float* __restrict__ scratch, uint32_t spw) {
+  using G = Geo<D>;
+  constexpr int KS = D / 64;  // K-steps of QK
+  constexpr int MB = D / 16;  // 16-dim blocks of PV
+  constexpr uint32_t W = D + 2;
+  constexpr uint32_t kImg = G::kBufBytes;
+  constexpr uint32_t kXBytes = 3u * 1024u;  // one block's weight digits of one tile: [digit][lane] x 16 bytes
+  constexpr uint32_t kXBase = kPcSlots * kImg;
+  static_assert(kXBase + kPcBlocks * 2u * kXBytes <= 160u * 1024u - 1024u, "LDS");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kXBase + kPcBlocks * 2u * kXBytes];
+  __shared__ float fx_s[kPcBlocks][2][17];  // [block][exchange slot]: f of head-rows 0-15, then 2^-kp
+  __shared__ uint32_t nvis_s[kPcBlocks];
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t n = lane & 15u, g = lane >> 4;
+  const uint32_t kv = blockIdx.y;
+  const uint32_t head_rows = a.rows * a.group, hblocks = (head_rows + 15u) / 16u;  // <= 3 (host-checked)
+  const bool dma = wave == 3u;
+  const bool qkw = wave < 3u;
+  const uint32_t blk = wave;                // QK waves: their head-row block
+  const bool has = qkw && blk < hblocks;    // wave-uniform
+
+  // Splits [sp0, sp1) of this work-group, tokens [s0, s1) (as the four-wave
+  // kernel; a split is a whole number of tiles).
+  const uint32_t sp0 = blockIdx.x * spw;
+  const uint32_t sp1 = sp0 + spw < a.splits ? sp0 + spw : a.splits;
+  const uint32_t tps = a.split_tokens / kTileTokens;  // tiles per split
+  const uint64_t s0_64 = uint64_t(a.begin) + uint64_t(sp0) * a.split_tokens;
+  const uint32_t s0 = s0_64 < a.end ? uint32_t(s0_64) : a.end;
+  const uint64_t s1_64 = uint64_t(a.begin) + uint64_t(sp1) * a.split_tokens;
+  const uint32_t s1 = s1_64 < a.end ? uint32_t(s1_64) : a.end;
+  const uint32_t k_first = s0 / kTileTokens;
+  const uint32_t ntiles = s1 > s0 ? (s1 - 1u) / kTileTokens + 1u - k_first : 0u;
+
+  // ---- DMA wave.
+  Ctx c;
+  PtCtx pc;
+  if (dma && ntiles > 0) {
+    c.k = kdata;
+    c.v = vdata;
+    c.ks = kscale;
+    c.vs = vscale;
+    c.table = table;
+    c.kv = kv;
+    c.kv_heads = a.kv_heads;
+    c.P = a.page_tokens;
+    c.pages = a.pages;
+    c.lp_lo = s0 / a.page_tokens;
+    c.lp_hi = (s1 - 1u) / a.page_tokens;
+    c.lane = lane;
+    const uint32_t lp = c.lp_lo + lane;
+    c.ptab = lp <= c.lp_hi ? table[lp] : 0u;
+    if constexpr (PT) {
+      const uint32_t kv_bytes = a.pages * a.kv_heads * a.page_tokens * uint32_t(D);
+      const uint32_t sc_bytes = a.pages * a.kv_heads * a.page_tokens * 4u;
+      pt_init<D>(pc, kdata, vdata, kscale, vscale, kv_bytes, sc_bytes, a.page_tokens, lane);
+    }
+  }
+  auto issue = [&](uint32_t t) __attribute__((always_inline)) {  // tile t of the range into slot t % 4
+    uint8_t* const buf = smem + (t % kPcSlots) * kImg;
+    const uint32_t k = k_first + t;
+    if constexpr (PT) {
+      const uint32_t lp = k * kTileTokens / a.page_tokens;
+      const uint32_t rel = lp - c.lp_lo;
+      uint32_t phys = rel < 64u ? __builtin_amdgcn_readlane(c.ptab, rel) : table[lp];
+      phys = phys < a.pages ? phys : a.pages - 1u;
+      pt_issue<D>(pc, phys * a.kv_heads + kv, k * kTileTokens - lp * a.page_tokens, a.page_tokens, buf);
+    } else {
+      part_issue<D, 1>(c, k, buf, 0u);
+    }
+  };
+  if (dma) {
+    if (ntiles > 0u) issue(0u);
+    if (ntiles > 1u) issue(1u);
+  }
+
+  // Per-lane LDS offsets inside a tile image (as the four-wave kernel).
+  const uint32_t lds_base = lds_addr(smem);
+  uint32_t koff[KS];
+  {
+    const uint32_t r0 = 16u * (n >> 2) + (n & 3u);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) koff[s] = r0 * D + 16u * ((4u * s + g) ^ swz_k<D>(r0));
+  }
+  const uint32_t voff = G::kKBytes + 64u * n + 16u * (g ^ swz_v(n));
+  const uint32_t soff = G::kKBytes + G::kVBytes + 64u * g;
+  const uint32_t vmoff = G::kKBytes + G::kVBytes + 256u + 4u * lane;
+
+  const uint32_t hr = blk * 16u + n;
+  const bool hvalid = has && hr < head_rows;
+  const uint32_t row = hvalid ? hr / a.group : 0u;
+  const uint32_t head = kv * a.group + (hvalid ? hr % a.group : 0u);
+  auto partial = [&](uint32_t sp) __attribute__((always_inline)) {
+    return scratch + ((size_t(row) * a.q_heads + head) * a.splits + sp) * W;
+  };
+
+  // The three roles run their own step loops (ntiles + 1 barriers each), so
+  // each role's registers live only in its own loop.
+  if (dma) {
+    // Tile s landed: the wave's loads are tiles s and s + 1, each exactly
+    // kLoadsPerTile vector-memory instructions when the page-table window
+    // covers the range (no table load inside an issue); else wait for all.
+    static_assert(G::kLoadsPerTile == 34u, "the tile's DMA instruction count");
+    const bool window = ntiles > 0u && c.lp_hi - c.lp_lo < 64u;
+    for (uint32_t s = 0; s <= ntiles; ++s) {
+      if (s < ntiles) {
+        if (s + 1u < ntiles && window) wait_vm<G::kLoadsPerTile>();
+        else wait_vm<0>();
+      }
+      __syncthreads();  // tile s visible to all; every wave is done with step s - 1
+      if (s + 2u < ntiles) issue(s + 2u);
+    }
+    return;
+  }
+  // Splits of this work-group past its last tile (a range that ends early,
+  // or no tile at all) get empty partials.
+  const uint32_t sp_e = ntiles > 0u ? sp0 + (ntiles - 1u) / tps + 1u : sp0;
+  if (qkw) {
+    // ---- QK waves: visibility and Q digits of the block.
+    uint32_t e_h = s0, e_min = s0, e_max = s0, nvis = 0;
+    float cs = 0.f;
+    i32x4 qd[3][KS];
+    if (has) {
+      float qv[KS][16];
+      int64_t klast = 0, qpos_l = INT64_MAX;  // lane i: query position of row r_lo + i
+      const uint32_t r_lo = blk * 16u / a.group;
+      const uint32_t r_hi = (blk * 16u + 15u < head_rows ? blk * 16u + 15u : head_rows - 1u) / a.group;
+      if (hvalid) {
+        const float* qp = q + (size_t(row) * a.q_heads + head) * D + 16u * g;
+  #pragma unroll
+        for (int s = 0; s < KS; ++s)
+  #pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float4 x = reinterpret_cast<const float4*>(qp + 64 * s)[j];
+            qv[s][4 * j] = x.x;
+            qv[s][4 * j + 1] = x.y;
+            qv[s][4 * j + 2] = x.z;
+            qv[s][4 * j + 3] = x.w;
+          }
+      } else {
+  #pragma unroll
+        for (int s = 0; s < KS; ++s)
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) qv[s][i] = 0.f;
+      }
+      if (s1 > s0) {
+        klast = kpos[s1 - 1u];
+        if (lane <= r_hi - r_lo) qpos_l = qpos[r_lo + lane];  // at most 16 rows per block
+        if (__ballot(klast > qpos_l) == 0) {  // every row of the block sees the whole range
+          e_h = s1;
+        } else {
+          for (uint32_t r = r_lo; r <= r_hi; ++r) {
+            const uint64_t xb = uint64_t(qpos_l);
+            const uint32_t xlo = __builtin_amdgcn_readlane(uint32_t(xb), r - r_lo);
+            const uint32_t xhi = __builtin_amdgcn_readlane(uint32_t(xb >> 32), r - r_lo);
+            const uint32_t e = visible_end(kpos, s0, s1, int64_t((uint64_t(xhi) << 32) | xlo), lane);
+            if (row == r) e_h = e;
+          }
+        }
+        if (!hvalid) e_h = s0;
+      }
+      uint32_t lo = hvalid ? e_h : 0xffffffffu, hi = e_h;
+  #define KVB_ROW_RED(N)                                                                                 \
+    {                                                                                                    \
+      const uint32_t o1 = uint32_t(__builtin_amdgcn_update_dpp(0, int(lo), 0x120 + N, 0xF, 0xF, false)); \
+      const uint32_t o2 = uint32_t(__builtin_amdgcn_update_dpp(0, int(hi), 0x120 + N, 0xF, 0xF, false)); \
+      lo = o1 < lo ? o1 : lo;                                                                            \
+      hi = o2 > hi ? o2 : hi;                                                                            \
+    }
+      KVB_ROW_RED(8) KVB_ROW_RED(4) KVB_ROW_RED(2) KVB_ROW_RED(1)
+  #undef KVB_ROW_RED
+      e_min = __builtin_amdgcn_readfirstlane(lo);
+      e_max = __builtin_amdgcn_readfirstlane(hi);
+      float amax = 0.f;
+  #pragma unroll
+      for (int s = 0; s < KS; ++s)
+  #pragma unroll
+        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(qv[s][i]));
+      amax = rows_max(amax);
+      int kq = 0;
+      if (amax > 0.f) {
+        kq = 22 - __builtin_amdgcn_frexp_expf(amax);  // |2^kq q| < 2^22: top digit in [-64, 64]
+        kq = kq < -100 ? -100 : (kq > 100 ? 100 : kq);
+      }
+  #pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        uint32_t w[3][4];
+  #pragma unroll
+        for (int i = 0; i < 4; ++i) w[0][i] = w[1][i] = w[2][i] = 0u;
+  #pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          int qi = int(__builtin_rintf(__builtin_amdgcn_ldexpf(qv[s][i], kq)));  // |qi| <= 2^22
+          if (a.scale < 0.f) qi = -qi;  // scores scale by |scale| (see cs)
+          const int lo8 = __builtin_amdgcn_sbfe(qi, 0, 8);
+          const int r1 = (qi - lo8) >> 8;
+          const int mid8 = __builtin_amdgcn_sbfe(r1, 0, 8);
+          const int hi8 = (r1 - mid8) >> 8;
+          w[0][i / 4] |= (uint32_t(hi8) & 0xffu) << (8 * (i % 4));
+          w[1][i / 4] |= (uint32_t(mid8) & 0xffu) << (8 * (i % 4));
+          w[2][i / 4] |= (uint32_t(lo8) & 0xffu) << (8 * (i % 4));
+        }
+  #pragma unroll
+        for (int dg = 0; dg < 3; ++dg) qd[dg][s] = i32x4{int(w[dg][0]), int(w[dg][1]), int(w[dg][2]), int(w[dg][3])};
+      }
+      cs = __builtin_amdgcn_ldexpf(fabsf(a.scale), -kq) * kLog2e;
+      cs = cs >= 1.17549435e-38f ? cs : 1.17549435e-38f;
+      nvis = e_max > s0 ? (e_max - 1u) / kTileTokens + 1u - k_first : 0u;
+      if (lane == 0) nvis_s[blk] = nvis;
+    }
+
+    float m_run = neg_inf(), l_run = 0.f;  // head-row h's running max (log2) and partial sum
+    // QK wave: tile t -> exchange slot t & 1.
+    auto qk_tile = [&](uint32_t t) __attribute__((always_inline)) {
+      const uint32_t pb = lds_base + (t % kPcSlots) * kImg;
+      uint32_t ka[KS];
+  #pragma unroll
+      for (int s = 0; s < KS; ++s) ka[s] = pb + koff[s];
+      const uint32_t sa = pb + soff, vma = pb + vmoff;
+      const uint32_t t0 = (k_first + t) * kTileTokens;
+      float sc[16];
+      float mx = neg_inf();
+      constexpr uint32_t NB = 4u;        // QK M-blocks of a tile
+      constexpr uint32_t kRd = KS + 1u;  // LDS reads per block
+      u32x4_t kr[3][KS], ksr[3];
+      auto read_k = [&](auto bc) __attribute__((always_inline)) {
+        constexpr uint32_t mb = decltype(bc)::value;
+        ds_issue_kblock<4u * mb * D, 16u * mb>(ka, sa, kr[mb % 3u], ksr[mb % 3u]);
+      };
+      i32x4 cq[2][3];
+      u32x4_t ksc[2];
+      const uint32_t vis = e_h > t0 ? (e_h - t0 < kTileTokens ? e_h - t0 : kTileTokens) : 0u;
+      const bool full = t0 + kTileTokens <= e_min;
+      auto qk = [&](auto maskc) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(maskc)::value;
+        auto scores = [&](auto bc) __attribute__((always_inline)) {
+          constexpr uint32_t mb = decltype(bc)::value;
+          const i32x4(&cc)[3] = cq[mb & 1u];
+          const u32x4_t ksm = ksc[mb & 1u];
+  #pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int hi2 = cc[0][e] * 256 + cc[1][e];  // |.| < 2^29
+            float s2 = fmaf(float(hi2), 256.f, float(cc[2][e])) * __uint_as_float(ksm[e]);
+            if constexpr (MASK) s2 = 16u * g + 4u * mb + e < vis ? s2 : neg_inf();
+            sc[4 * mb + e] = s2;
+            mx = fmaxf(mx, s2);
+          }
+  #pragma unroll
+          for (int e = 0; e < 4; ++e) pin(sc[4 * mb + e]);
+        };
+        read_k(std::integral_constant<uint32_t, 0>{});
+        read_k(std::integral_constant<uint32_t, 1>{});
+        static_for<0, NB>([&](auto bc) __attribute__((always_inline)) {
+          constexpr uint32_t mb = decltype(bc)::value;
+          if constexpr (mb + 1 < NB) wait_lgkm<kRd>();
+          else wait_lgkm<0>();
+  #pragma unroll
+          for (int st = 0; st < KS; ++st) pin(kr[mb % 3u][st]);
+          pin(ksr[mb % 3u]);
+          ksc[mb & 1u] = ksr[mb % 3u];
+          if constexpr (mb + 2 < NB) read_k(std::integral_constant<uint32_t, mb + 2>{});
+          i32x4(&cc)[3] = cq[mb & 1u];
+  #pragma unroll
+          for (int dg = 0; dg < 3; ++dg) cc[dg] = i32x4{0, 0, 0, 0};
+  #pragma unroll
+          for (int st = 0; st < KS; ++st) {
+            const u32x4_t& k4 = kr[mb % 3u][st];
+            const i32x4 av = {int(k4[0]), int(k4[1]), int(k4[2]), int(k4[3])};
+  #pragma unroll
+            for (int dg = 0; dg < 3; ++dg)
+              cc[dg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, qd[dg][st], cc[dg], 0, 0, 0);
+          }
+          if constexpr (mb > 0) {
+            scores(std::integral_constant<uint32_t, mb - 1>{});
+  #pragma unroll
+            for (int i = 0; i < 3 * KS; ++i) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+              __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // then up to three VALU
+            }
+          }
+        });
+        scores(std::integral_constant<uint32_t, NB - 1>{});
+      };
+      if (full) qk(std::false_type{});
+      else qk(std::true_type{});
+      pin(mx);
+
+      // v-scales of the tile (lane = token), running maximum, weight exponent kp.
+      const float v = __uint_as_float(ds_read4_sync<0>(vma));
+      const float vm = t0 + lane < e_max ? fabsf(v) : 0.f;
+      const float m_new = fmaxf(m_run, rows_max(mx) * cs);
+      const float vmax = wave_max(vm);
+      int kp = 0;
+      if (vmax > 0.f) {
+        kp = 21 - __builtin_amdgcn_frexp_expf(vmax * kVmaxMargin);
+        kp = kp < -100 ? -100 : (kp > 100 ? 100 : kp);
+      }
+      const float f = m_run == neg_inf() ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      const float mu = (m_new == neg_inf() ? 0.f : m_new) - float(kp);  // 2^(s - mu) = w * 2^kp
+      m_run = m_new;
+
+      // Weights as three 7-bit digits (k-position = token 16g + 4mb + e); slots
+      // past the block's last visible token get a zero v-scale.
+      const uint32_t vlim = e_max > t0 ? (e_max - t0 < kTileTokens ? e_max - t0 : kTileTokens) : 0u;
+      const bool vfull = t0 + kTileTokens <= e_max;
+      i32x4 bd[3];
+      float lw = 0.f;
+      auto weights = [&](auto maskc) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(maskc)::value;
+        u32x4_t vsr[4];  // v-scales of tokens 16g .. 16g + 15
+        ds_read16x4<256u, 272u, 288u, 304u>(sa, vsr[0], vsr[1], vsr[2], vsr[3]);
+        uint32_t bw[3][4];
+  #pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          bw[0][mb] = bw[1][mb] = bw[2][mb] = 0u;
+  #pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float w = __builtin_amdgcn_exp2f(fmaf(sc[4 * mb + e], cs, -mu));  // w * 2^kp
+            lw += w;
+            float vsl = __uint_as_float(vsr[mb][e]);
+            if constexpr (MASK) vsl = 16u * g + 4u * mb + e < vlim ? vsl : 0.f;
+            const uint32_t pbits = __float_as_uint(fmaf(w, vsl, 12582912.f));  // see the four-wave kernel
+            bw[0][mb] |= ((pbits >> 14) & 0xffu) << (8 * e);
+            bw[1][mb] |= ((pbits >> 7) & 0x7fu) << (8 * e);
+            bw[2][mb] |= (pbits & 0x7fu) << (8 * e);
+          }
+        }
+  #pragma unroll
+        for (int dg = 0; dg < 3; ++dg) bd[dg] = i32x4{int(bw[dg][0]), int(bw[dg][1]), int(bw[dg][2]), int(bw[dg][3])};
+      };
+      if (vfull) weights(std::false_type{});
+      else weights(std::true_type{});
+      const float inv = __builtin_amdgcn_ldexpf(1.f, -kp);
+      l_run = fmaf(lw, inv, l_run * f);
+      uint8_t* const xb = smem + kXBase + (blk * 2u + (t & 1u)) * kXBytes;
+  #pragma unroll
+      for (int dg = 0; dg < 3; ++dg) *reinterpret_cast<i32x4*>(xb + 1024u * dg + 16u * lane) = bd[dg];
+      if (g == 0) fx_s[blk][t & 1u][n] = f;
+      if (lane == 0) fx_s[blk][t & 1u][16] = inv;
+    };
+
+    auto write_ml = [&](uint32_t sp) __attribute__((always_inline)) {
+      const float l_h = rows_sum(l_run);
+      if (hvalid && g == 0) {
+        float* const dst = partial(sp);
+        dst[0] = m_run * kLn2;
+        dst[1] = l_h;
+      }
+      m_run = neg_inf();
+      l_run = 0.f;
+    };
+    for (uint32_t s = 0; s <= ntiles; ++s) {
+      __syncthreads();
+      if (has && s < ntiles) {
+        if (s < nvis) qk_tile(s);
+        if (s % tps == tps - 1u || s + 1u == ntiles) write_ml(sp0 + s / tps);
+      }
+    }
+    if (has)
+      for (uint32_t sp = sp_e; sp < sp1; ++sp) write_ml(sp);
+    return;
+  }
+  // PV waves: wave 4 + j takes the 16-dim blocks 4j .. 4j + 3 of every
+  // head-row block (the V rows it reads serve all three blocks), so the PV
+  // work of the blocks is spread over all four SIMDs.
+  const uint32_t pj = wave - 4u;
+  f32x4 acc[kPcBlocks][4];  // [block][m]: lane (h, g): dims 16 (4j + m) + 4g + e
+#pragma unroll
+  for (uint32_t b = 0; b < kPcBlocks; ++b)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc[b][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto pv_tile = [&](uint32_t t) __attribute__((always_inline)) {
+    const uint32_t va = lds_base + (t % kPcSlots) * kImg + voff + 4096u * pj;
+    const uint32_t xs = t & 1u;
+    // A block this tile does not reach (past its visible range, or absent)
+    // gets zero digits, f = 1 and 2^-kp = 0, so its numerators stay as they
+    // are and the pipeline has no branch.
+    i32x4 bd[kPcBlocks][3];
+    float f[kPcBlocks], inv[kPcBlocks];
+#pragma unroll
+    for (uint32_t b = 0; b < kPcBlocks; ++b) {
+      const bool live = b < hblocks && t < nvis_s[b];
+      const uint8_t* const xb = smem + kXBase + (b * 2u + xs) * kXBytes;
+#pragma unroll
+      for (int dg = 0; dg < 3; ++dg)
+        bd[b][dg] = live ? *reinterpret_cast<const i32x4*>(xb + 1024u * dg + 16u * lane) : i32x4{0, 0, 0, 0};
+      f[b] = live ? fx_s[b][xs][n] : 1.f;
+      inv[b] = live ? fx_s[b][xs][16] : 0.f;
+    }
+#pragma unroll
+    for (uint32_t b = 0; b < kPcBlocks; ++b)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) acc[b][m] *= f[b];  // exact where f == 1
+    u32x4_t vr[4];
+    ds_issue16x1<0u>(va, vr[0]);
+    ds_issue16x1<1024u>(va, vr[1]);
+    ds_issue16x1<2048u>(va, vr[2]);
+    ds_issue16x1<3072u>(va, vr[3]);
+    i32x4 cv[2][3];
+    // unit u: dim block m = u / 3 of head-row block b = u % 3; its MFMAs
+    // run with the previous unit's fold
+    auto fold = [&](auto uc) __attribute__((always_inline)) {
+      constexpr uint32_t u = decltype(uc)::value, m = u / 3u, b = u % 3u;
+      const i32x4(&cc)[3] = cv[u & 1u];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int hi2 = cc[0][e] * 128 + cc[1][e];  // |.| < 2^29
+        acc[b][m][e] = fmaf(fmaf(float(hi2), 128.f, float(cc[2][e])), inv[b], acc[b][m][e]);
+      }
+    };
+    static_for<0, 12>([&](auto uc) __attribute__((always_inline)) {
+      constexpr uint32_t u = decltype(uc)::value, m = u / 3u, b = u % 3u;
+      if constexpr (b == 0u) {
+        wait_lgkm<3u - m>();  // dim block m's V rows landed; the later ones may be in flight
+        pin(vr[m]);
+      }
+      i32x4(&cc)[3] = cv[u & 1u];
+      const i32x4 av = {int(vr[m][0]), int(vr[m][1]), int(vr[m][2]), int(vr[m][3])};
+#pragma unroll
+      for (int dg = 0; dg < 3; ++dg) cc[dg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bd[b][dg], i32x4{0, 0, 0, 0}, 0, 0, 0);
+      if constexpr (u > 0) {
+        fold(std::integral_constant<uint32_t, u - 1>{});
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // then up to four VALU
+        }
+      }
+    });
+    fold(std::integral_constant<uint32_t, 11>{});
+  };
+
+  auto write_n = [&](uint32_t sp) __attribute__((always_inline)) {
+#pragma unroll
+    for (uint32_t b = 0; b < kPcBlocks; ++b) {
+      const uint32_t hrb = b * 16u + n;
+      if (b < hblocks && hrb < head_rows) {
+        const uint32_t rowb = hrb / a.group, headb = kv * a.group + hrb % a.group;
+        float* const dst = scratch + ((size_t(rowb) * a.q_heads + headb) * a.splits + sp) * W + 2 + 64u * pj;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dst[16 * m + 4 * g + e] = acc[b][m][e];
+      }
+#pragma unroll
+      for (int m = 0; m < 4; ++m) acc[b][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+
+  for (uint32_t s = 0; s <= ntiles; ++s) {
+    __syncthreads();
+    if (s > 0u) {
+      const uint32_t t = s - 1u;
+      pv_tile(t);
+      if (t % tps == tps - 1u || t + 1u == ntiles) write_n(sp0 + t / tps);
+    }
+  }
+  for (uint32_t sp = sp_e; sp < sp1; ++sp) write_n(sp);
+}
+
 #define KVB_I8R_ARGS                                                                             \
   a, a.q, a.q_positions, a.k_positions, a.page_table, static_cast<const int8_t*>(a.k),             \
       static_cast<const int8_t*>(a.v), a.k_scales, a.v_scales, a.scratch, spw
@@ -740,6 +1240,13 @@ uint32_t device_cus() {
   return v;
 }
 
+// The wave-specialized kernel: dim 256 and one round of at most three
+// head-row blocks (17 to 48 head-rows).
+bool pc_shape(const SplitArgs& a) {
+  const uint32_t hblocks = (a.rows * a.group + 15u) / 16u;
+  return a.dim == 256 && hblocks <= kPcBlocks;
+}
+
 template <int D>
 hipError_t launch_dim(const SplitArgs& a, hipStream_t stream) {
   // Short splits: several consecutive splits per work-group (one work-group
@@ -750,7 +1257,17 @@ hipError_t launch_dim(const SplitArgs& a, hipStream_t stream) {
     spw = per_cu > 1u ? per_cu : 1u;
   }
   const dim3 grid((a.splits + spw - 1u) / spw, a.kv_heads);
-  if (a.page_tokens % kTileTokens == 0)
+  const bool pt = a.page_tokens % kTileTokens == 0;
+  if constexpr (D == 256) {
+    if (pc_shape(a)) {
+      if (pt)
+        hipLaunchKernelGGL((split_i8_rows_pc_kernel<D, true>), grid, dim3(64 * kPcWaves), 0, stream, KVB_I8R_ARGS);
+      else
+        hipLaunchKernelGGL((split_i8_rows_pc_kernel<D, false>), grid, dim3(64 * kPcWaves), 0, stream, KVB_I8R_ARGS);
+      return hipGetLastError();
+    }
+  }
+  if (pt)
     hipLaunchKernelGGL((split_i8_rows_kernel<D, true>), grid, dim3(64 * kWaves), 0, stream, KVB_I8R_ARGS);
   else
     hipLaunchKernelGGL((split_i8_rows_kernel<D, false>), grid, dim3(64 * kWaves), 0, stream, KVB_I8R_ARGS);
@@ -761,8 +1278,12 @@ template <int D>
 hipError_t preload_dim() {
   hipFuncAttributes attr{};
   hipError_t e = hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_i8_rows_kernel<D, true>));
-  if (e != hipSuccess) return e;
-  return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_i8_rows_kernel<D, false>));
+  if (e == hipSuccess) e = hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_i8_rows_kernel<D, false>));
+  if constexpr (D == 256) {
+    if (e == hipSuccess) e = hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_i8_rows_pc_kernel<D, true>));
+    if (e == hipSuccess) e = hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_i8_rows_pc_kernel<D, false>));
+  }
+  return e;
 }
 
 }  // namespace
@@ -785,8 +1306,8 @@ hipError_t launch_split_i8_rows(const SplitArgs& a, hipStream_t stream) {
 
 const char* i8_rows_kernel_name(const SplitArgs& a) {
   static thread_local char buf[96];
-  std::snprintf(buf, sizeof(buf), "split_i8_rows_kernel<%u,%s>", a.dim,
-                a.page_tokens % kTileTokens == 0 ? "true" : "false");
+  std::snprintf(buf, sizeof(buf), "%s<%u,%s>", pc_shape(a) ? "split_i8_rows_pc_kernel" : "split_i8_rows_kernel",
+                a.dim, a.page_tokens % kTileTokens == 0 ? "true" : "false");
   return buf;
 }
 

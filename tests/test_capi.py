@@ -86,8 +86,8 @@ def test_kernel_choice_for_the_dense_mma_geometry():
     inp = kvb.device_input(fake, fake, fake, fake, fake, fake, fake, fake)
     s = kvb.make_shape(8, 24, 4, 256, 32, 2048, 65536, 0, 65536, 0.0625)
     assert kvb.attention_mma_supported(s)
-    assert kvb.selected_kernel_name(s, inp, 256) == "split_i8_rows_kernel<256,false>"
-    assert kvb.selected_kernel_name(s, inp, 1024) == "split_i8_rows_kernel<256,false>"
+    assert kvb.selected_kernel_name(s, inp, 256) == "split_i8_rows_pc_kernel<256,false>"
+    assert kvb.selected_kernel_name(s, inp, 1024) == "split_i8_rows_pc_kernel<256,false>"
     assert kvb.selected_kernel_name(s, inp, 1000).startswith("split_lds_kernel<256,")  # off-tile split size
     assert kvb.selected_kernel_name(s.copy(begin=32), inp, 256).startswith("split_lds_kernel<256,")  # off-tile start
     s128 = kvb.make_shape(8, 48, 8, 128, 64, 10, 640, 64, 640, 0.0883883)

@@ -137,6 +137,12 @@ I8_ROWS_SHAPES = [
     (8, 24, 4, 256, 32, 32768, 0, 32768, 256, "causal", 0.0),  # 128 splits x 4 kv: two splits each
     (4, 32, 8, 128, 64, 20000, 0, 19900, 256, "spread", 0.01),  # 78 splits x 8 kv, ragged last split
     (8, 96, 4, 128, 64, 40000, 128, 40000, 256, "masked", 0.0),  # 192 head-rows (3 streams) x 2 splits each
+    # dim 256 beyond three head-row blocks: the four-wave kernel
+    (8, 96, 8, 256, 64, 2048, 0, 2048, 512, "causal", 0.0),    # 96 head-rows: two streams of 4 / 2 blocks
+    (4, 64, 4, 256, 32, 1500, 64, 1500, 320, "spread", 0.02),  # 64 head-rows: one round of 4 blocks
+    # dim 256, one to three blocks: the wave-specialized kernel at more shapes
+    (1, 18, 1, 256, 64, 777, 0, 777, 128, "causal", 0.0),      # 18 head-rows, one kv head, ragged tail
+    (6, 40, 5, 256, 16, 3000, 128, 2900, 1024, "masked", 0.01),  # 48 head-rows, 16-token pages, masked rows
 ]
 
 
@@ -163,7 +169,9 @@ def test_i8_rows_kernel_shapes(gpu, cfg):
     case = W.synth_case(rows, qh, kvh, d, p, t, seed=seed, begin=b, end=e, qpos=qpos, outlier_frac=outl)
     name = kvb.selected_kernel_name(case.shape, kvb.device_input(*([0x1000] * 8)), st)
     log(f"i8 rows shape={case.shape.as_tuple()} split_tokens={st} qpos={kind} kernel={name}")
-    assert name.startswith("split_i8_rows_kernel<"), name
+    hblocks = (rows * (qh // kvh) + 15) // 16
+    family = "split_i8_rows_pc_kernel<" if d == 256 and hblocks <= 3 else "split_i8_rows_kernel<"
+    assert name.startswith(family), name
     dc = DeviceCase(case)
     ref = O.fp64(case, threads=8)
     # The per-element gate is asserted wherever the fp32 restatement of the
@@ -188,7 +196,8 @@ def test_i8_rows_kernel_shapes(gpu, cfg):
 SCALE_SHAPES = [
     # rows, q_heads, kv_heads, dim, P, tokens, split_tokens, kernel family
     (1, 8, 2, 128, 64, 2048, 512, "split_i8_kernel<"),
-    (8, 24, 4, 256, 32, 2048, 256, "split_i8_rows_kernel<"),
+    (8, 24, 4, 256, 32, 2048, 256, "split_i8_rows_pc_kernel<"),
+    (8, 96, 8, 256, 64, 2048, 512, "split_i8_rows_kernel<"),
     (4, 24, 4, 64, 16, 1000, 256, "split_lds_rows_kernel<"),
 ]
 
@@ -318,7 +327,8 @@ WIDE_Q_SHAPES = [
     (1, 32, 8, 128, 64, 8192, 2048, "split_i8_kernel<"),     # cfg2 geometry (paired-row QK)
     (1, 8, 2, 64, 16, 512, 128, "split_i8_kernel<"),         # cfg1 geometry (small-page path)
     (1, 64, 8, 128, 64, 4096, 1024, "split_i8_kernel<"),     # 8 head-rows per kv head
-    (8, 24, 4, 256, 32, 2048, 256, "split_i8_rows_kernel<"),  # dense rows-8 / group-6 geometry
+    (8, 24, 4, 256, 32, 2048, 256, "split_i8_rows_pc_kernel<"),  # dense rows-8 / group-6 geometry
+    (8, 96, 8, 256, 64, 2048, 512, "split_i8_rows_kernel<"),     # 96 head-rows at dim 256
 ]
 
 

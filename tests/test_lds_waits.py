@@ -44,6 +44,31 @@ def test_scanner_accepts_waited_reads_and_other_lgkm_ops():
     assert C.scan_asm(asm) == {}
 
 
+def test_scanner_follows_branches():
+    """A read pending in an out-of-line block reaches only that block's
+    successors: the block after its unconditional branch in file order is
+    not one, its branch target is."""
+    asm = """_Zcfg:
+\ts_cbranch_vccz .LBB0_3
+\ts_cbranch_scc1 .LBB0_2
+\ts_endpgm
+.LBB0_2:
+\tds_read_b128 v[8:11], v1
+\ts_branch .LBB0_4
+.LBB0_3:
+\tv_mov_b32_e32 v22, v8
+\ts_endpgm
+.LBB0_4:
+\tv_mov_b32_e32 v23, v9
+\ts_waitcnt lgkmcnt(0)
+\tv_mov_b32_e32 v24, v10
+\ts_endpgm
+.Lfunc_end2:
+"""
+    found = C.scan_asm(asm)["_Zcfg"]
+    assert [t for _, t in found] == ["v_mov_b32_e32 v23, v9"]
+
+
 @pytest.mark.timeout(900)
 def test_every_kernel_waits_before_using_lds_reads():
     with tempfile.TemporaryDirectory() as tmp:
