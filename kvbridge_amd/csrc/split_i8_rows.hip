@@ -171,6 +171,9 @@ template <uint32_t O0>
 __device__ __forceinline__ void ds_issue16x1(uint32_t a, u32x4_t& r0) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(r0) : "v"(a), "i"(O0) : "memory");
 }
+// s_barrier without the memory fences of __syncthreads (no wait for the
+// wave's own loads before it); the asm keeps memory accesses on their side.
+__device__ __forceinline__ void bare_barrier() { asm volatile("s_barrier" ::: "memory"); }
 template <uint32_t N>
 __device__ __forceinline__ void wait_lgkm() { asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory"); }
 
@@ -741,14 +744,15 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
 //    barrier, then tile s + 2 goes into slot (s + 2) % 4 (two tiles of lead;
 //    that slot held tile s - 2, whose last reader, PV step s - 1, is behind
 //    the barrier);
-//  - QK wave: scores of tile s, running maximum, the weights' three 7-bit
-//    digits (B of PV) into its exchange slot s & 1 with the rescale factor f
-//    of each head-row and 2^-kp;
+//  - QK wave: scores of tile s, running maximum, the weights' three int8
+//    digits in base 256 (B of PV; the two low ones balanced) into its
+//    exchange slot s & 1 with the rescale factor f of each head-row and 2^-kp;
 //  - PV waves: tile s - 1 from the other exchange slots, acc = acc * f +
 //    (V . P) * 2^-kp per block.
 // One barrier per step.  The arithmetic is the four-wave kernel's per
 // 64-token step instead of per 128-token phase (running maximum, kp and the
-// digit fold per tile), so the partials agree with it to rounding.  The QK
+// digit fold per tile), with the same integer weights p split into
+// byte-aligned digits, so the partials agree with it to rounding.  The QK
 // wave owns m and l of its block's head-rows and the PV waves the
 // numerators; each writes its part of a split's partial after the split's
 // last tile.
@@ -832,10 +836,6 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
       part_issue<D, 1>(c, k, buf, 0u);
     }
   };
-  if (dma) {
-    if (ntiles > 0u) issue(0u);
-    if (ntiles > 1u) issue(1u);
-  }
 
   // Per-lane LDS offsets inside a tile image (as the four-wave kernel).
   const uint32_t lds_base = lds_addr(smem);
@@ -865,6 +865,12 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
     // covers the range (no table load inside an issue); else wait for all.
     static_assert(G::kLoadsPerTile == 34u, "the tile's DMA instruction count");
     const bool window = ntiles > 0u && c.lp_hi - c.lp_lo < 64u;
+    // The QK waves' own loads (Q, positions) go out first, chip-wide ahead
+    // of the tiles, so their round trip does not queue behind the DMA (a
+    // bare s_barrier: no wait for those loads).
+    bare_barrier();
+    if (ntiles > 0u) issue(0u);
+    if (ntiles > 1u) issue(1u);
     for (uint32_t s = 0; s <= ntiles; ++s) {
       if (s < ntiles) {
         if (s + 1u < ntiles && window) wait_vm<G::kLoadsPerTile>();
@@ -883,6 +889,7 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
     uint32_t e_h = s0, e_min = s0, e_max = s0, nvis = 0;
     float cs = 0.f;
     i32x4 qd[3][KS];
+    if (!has) bare_barrier();  // the prologue barrier (see the DMA wave)
     if (has) {
       float qv[KS][16];
       int64_t klast = 0, qpos_l = INT64_MAX;  // lane i: query position of row r_lo + i
@@ -909,6 +916,10 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
       if (s1 > s0) {
         klast = kpos[s1 - 1u];
         if (lane <= r_hi - r_lo) qpos_l = qpos[r_lo + lane];  // at most 16 rows per block
+      }
+      bare_barrier();  // the loads above are out: the DMA wave may start
+      asm volatile("" : "+v"(klast), "+v"(qpos_l));  // their uses (and waits) stay after the barrier
+      if (s1 > s0) {
         if (__ballot(klast > qpos_l) == 0) {  // every row of the block sees the whole range
           e_h = s1;
         } else {
@@ -1061,8 +1072,8 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
       const float mu = (m_new == neg_inf() ? 0.f : m_new) - float(kp);  // 2^(s - mu) = w * 2^kp
       m_run = m_new;
 
-      // Weights as three 7-bit digits (k-position = token 16g + 4mb + e); slots
-      // past the block's last visible token get a zero v-scale.
+      // Weights as three base-256 int8 digits (k-position = token 16g + 4mb +
+      // e); slots past the block's last visible token get a zero v-scale.
       const uint32_t vlim = e_max > t0 ? (e_max - t0 < kTileTokens ? e_max - t0 : kTileTokens) : 0u;
       const bool vfull = t0 + kTileTokens <= e_max;
       i32x4 bd[3];
@@ -1074,18 +1085,28 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
         uint32_t bw[3][4];
   #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
-          bw[0][mb] = bw[1][mb] = bw[2][mb] = 0u;
+          uint32_t x[4];
   #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float w = __builtin_amdgcn_exp2f(fmaf(sc[4 * mb + e], cs, -mu));  // w * 2^kp
             lw += w;
             float vsl = __uint_as_float(vsr[mb][e]);
             if constexpr (MASK) vsl = 16u * g + 4u * mb + e < vlim ? vsl : 0.f;
-            const uint32_t pbits = __float_as_uint(fmaf(w, vsl, 12582912.f));  // see the four-wave kernel
-            bw[0][mb] |= ((pbits >> 14) & 0xffu) << (8 * e);
-            bw[1][mb] |= ((pbits >> 7) & 0x7fu) << (8 * e);
-            bw[2][mb] |= (pbits & 0x7fu) << (8 * e);
+            // p = w * v_scale rounded to an integer (0 <= p < 2^21): t = 2^23 +
+            // 0x8080 + p lies in [2^23, 2^24), where the float's ulp is 1, so
+            // its mantissa bits are q = p + 0x8080 and p = (q2 << 16) + ((q1 -
+            // 128) << 8) + (q0 - 128) with q's bytes q2 (0 .. 32) and q1, q0:
+            // the digits are byte 2 and bytes 1, 0 xor 0x80 (int8).
+            x[e] = __float_as_uint(fmaf(w, vsl, 8421504.f));
           }
+          // 4 x 3 byte transpose: digit k of the four tokens into one word.
+          const uint32_t lo01 = __builtin_amdgcn_perm(x[1], x[0], 0x05010400u);  // x0.b0 x1.b0 x0.b1 x1.b1
+          const uint32_t lo23 = __builtin_amdgcn_perm(x[3], x[2], 0x05010400u);
+          const uint32_t hi01 = __builtin_amdgcn_perm(x[1], x[0], 0x0c0c0602u);  // x0.b2 x1.b2 0 0
+          const uint32_t hi23 = __builtin_amdgcn_perm(x[3], x[2], 0x06020c0cu);  // 0 0 x2.b2 x3.b2
+          bw[0][mb] = hi01 | hi23;
+          bw[1][mb] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
+          bw[2][mb] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
         }
   #pragma unroll
         for (int dg = 0; dg < 3; ++dg) bd[dg] = i32x4{int(bw[dg][0]), int(bw[dg][1]), int(bw[dg][2]), int(bw[dg][3])};
@@ -1126,6 +1147,7 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
   // head-row block (the V rows it reads serve all three blocks), so the PV
   // work of the blocks is spread over all four SIMDs.
   const uint32_t pj = wave - 4u;
+  bare_barrier();  // the prologue barrier (see the DMA wave)
   f32x4 acc[kPcBlocks][4];  // [block][m]: lane (h, g): dims 16 (4j + m) + 4g + e
 #pragma unroll
   for (uint32_t b = 0; b < kPcBlocks; ++b)
@@ -1151,8 +1173,9 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
     }
 #pragma unroll
     for (uint32_t b = 0; b < kPcBlocks; ++b)
+      if (__builtin_amdgcn_ballot_w64(f[b] != 1.f) != 0u)  // skipped where no maximum of the block rose
 #pragma unroll
-      for (int m = 0; m < 4; ++m) acc[b][m] *= f[b];  // exact where f == 1
+        for (int m = 0; m < 4; ++m) acc[b][m] *= f[b];
     u32x4_t vr[4];
     ds_issue16x1<0u>(va, vr[0]);
     ds_issue16x1<1024u>(va, vr[1]);
@@ -1166,8 +1189,8 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
       const i32x4(&cc)[3] = cv[u & 1u];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int hi2 = cc[0][e] * 128 + cc[1][e];  // |.| < 2^29
-        acc[b][m][e] = fmaf(fmaf(float(hi2), 128.f, float(cc[2][e])), inv[b], acc[b][m][e]);
+        const int hi2 = cc[0][e] * 256 + cc[1][e];  // digits in base 256: |.| < 2^27
+        acc[b][m][e] = fmaf(fmaf(float(hi2), 256.f, float(cc[2][e])), inv[b], acc[b][m][e]);
       }
     };
     static_for<0, 12>([&](auto uc) __attribute__((always_inline)) {
