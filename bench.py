@@ -76,6 +76,8 @@ def main():
     ap.add_argument("--no-batched", action="store_true", help="skip the batched configs[2] / configs[3] timings")
     ap.add_argument("--no-mma-geometry", action="store_true",
                     help="skip the rows-8 / group-6 / dim-256 / page-32 launch_attention_mma timing")
+    ap.add_argument("--mma-calls", choices=("both", "launch_attention_mma", "decode_1024_token_splits"),
+                    default="both", help="which dense-geometry calls to time (profiling runs select one)")
     ap.add_argument("--no-append", action="store_true", help="skip the paged INT8 append timings")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run known-size copy and read kernels (for scaling rocprofv3 byte counters)")
@@ -572,6 +574,8 @@ def main():
                 ("decode_1024_token_splits", lambda i: kvb.decode_attention(ms_, minps[i % copies], dst_, msc, mm_,
                                                                             ml_, mn_, stream=sp),
                  kvb.split_count(ms_, dst_))):
+            if args.mma_calls not in ("both", key):
+                continue
             rec = {"splits": nspl}
             fn_(0)
             torch.cuda.synchronize()
