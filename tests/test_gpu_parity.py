@@ -143,6 +143,7 @@ I8_ROWS_SHAPES = [
     # dim 256, one to three blocks: the wave-specialized kernel at more shapes
     (1, 18, 1, 256, 64, 777, 0, 777, 128, "causal", 0.0),      # 18 head-rows, one kv head, ragged tail
     (6, 40, 5, 256, 16, 3000, 128, 2900, 1024, "masked", 0.01),  # 48 head-rows, 16-token pages, masked rows
+    (8, 24, 4, 256, 32, 40000, 0, 39900, 256, "causal", 0.0),  # 156 splits x 4 kv: two per work-group, ragged end
 ]
 
 
