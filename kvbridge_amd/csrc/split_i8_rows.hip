@@ -759,6 +759,7 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
 constexpr uint32_t kPcBlocks = 3;
 constexpr uint32_t kPcWaves = 8;
 constexpr uint32_t kPcSlots = 4;
+constexpr float kPcHeadroom = 2.f;  // log2 units of maximum growth an epoch absorbs
 
 template <int D, bool PT>
 __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
@@ -775,7 +776,10 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
   constexpr uint32_t kXBase = kPcSlots * kImg;
   static_assert(kXBase + kPcBlocks * 2u * kXBytes <= 160u * 1024u - 1024u, "LDS");
   __shared__ __attribute__((aligned(16))) uint8_t smem[kXBase + kPcBlocks * 2u * kXBytes];
-  __shared__ float fx_s[kPcBlocks][2][17];  // [block][exchange slot]: f of head-rows 0-15, then 2^-kp
+  // [block][exchange slot]: a tile's epoch fold (f of head-rows 0-15, 2^-kp
+  // of the epoch ending, flag) and a split's end (e of head-rows 0-15 at
+  // 18-33, 2^-kp of its last epoch at 34)
+  __shared__ float fx_s[kPcBlocks][2][36];
   __shared__ uint32_t nvis_s[kPcBlocks];
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -983,6 +987,20 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
     }
 
     float m_run = neg_inf(), l_run = 0.f;  // head-row h's running max (log2) and partial sum
+    // Scale epochs: the weights of all tiles of an epoch use one reference R
+    // per head-row (the running maximum at the epoch's first tile plus
+    // kPcHeadroom) and one v-scale exponent kp, so the PV waves add the
+    // epoch's int32 digit sums in the MFMA accumulators and fold them into
+    // fp32 only when it ends.  A tile starts a new epoch when a head-row's
+    // maximum passes its R, when its largest v-scale leaves [vlo, vcap) (a
+    // quarter of the epoch's first, and the largest that keeps every weight
+    // integer below 2^23 - 2^16), or after 1,024 tiles (the int32 range of
+    // the digit sums).  l_run is in units of 2^(s - R).
+    float R = neg_inf();
+    int kp = 0;
+    float vcap = 0.f, vlo = 0.f;
+    uint32_t epoch_tiles = 0;
+    bool epoch = false;
     // QK wave: tile t -> exchange slot t & 1.
     auto qk_tile = [&](uint32_t t) __attribute__((always_inline)) {
       const uint32_t pb = lds_base + (t % kPcSlots) * kImg;
@@ -1063,14 +1081,34 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
       const float vm = t0 + lane < e_max ? fabsf(v) : 0.f;
       const float m_new = fmaxf(m_run, rows_max(mx) * cs);
       const float vmax = wave_max(vm);
-      int kp = 0;
-      if (vmax > 0.f) {
-        kp = 21 - __builtin_amdgcn_frexp_expf(vmax * kVmaxMargin);
-        kp = kp < -100 ? -100 : (kp > 100 ? 100 : kp);
+      float* const fx = fx_s[blk][t & 1u];
+      const bool rise = __builtin_amdgcn_ballot_w64(m_new > R) != 0u;
+      if (!epoch || rise || vmax >= vcap || vmax < vlo || epoch_tiles >= 1024u) {
+        int kp_new = 100;  // no v-scale yet: any later one starts an epoch
+        if (vmax > 0.f) {
+          kp_new = 22 - __builtin_amdgcn_frexp_expf(vmax * kVmaxMargin);  // vmax * 2^kp < 2^22
+          kp_new = kp_new < -100 ? -100 : (kp_new > 100 ? 100 : kp_new);
+        }
+        const float r_new = m_new == neg_inf() ? neg_inf() : m_new + kPcHeadroom;
+        const float f = R == neg_inf() ? 0.f : __builtin_amdgcn_exp2f(R - r_new);  // <= 1
+        l_run *= f;
+        if (g == 0) fx[n] = f;
+        if (lane == 0) {
+          fx[16] = epoch ? __builtin_amdgcn_ldexpf(1.f, -kp) : 0.f;
+          fx[17] = 1.f;
+        }
+        R = r_new;
+        kp = kp_new;
+        vcap = __builtin_amdgcn_ldexpf(0.9921875f, 23 - kp_new);
+        vlo = 0.25f * vmax;
+        epoch_tiles = 0;
+        epoch = true;
+      } else if (lane == 0) {
+        fx[17] = 0.f;
       }
-      const float f = m_run == neg_inf() ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-      const float mu = (m_new == neg_inf() ? 0.f : m_new) - float(kp);  // 2^(s - mu) = w * 2^kp
+      ++epoch_tiles;
       m_run = m_new;
+      const float mu = (R == neg_inf() ? 0.f : R) - float(kp);  // 2^(s - mu) = w * 2^kp, w <= 1
 
       // Weights as three base-256 int8 digits (k-position = token 16g + 4mb +
       // e); slots past the block's last visible token get a zero v-scale.
@@ -1092,11 +1130,11 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
             lw += w;
             float vsl = __uint_as_float(vsr[mb][e]);
             if constexpr (MASK) vsl = 16u * g + 4u * mb + e < vlim ? vsl : 0.f;
-            // p = w * v_scale rounded to an integer (0 <= p < 2^21): t = 2^23 +
-            // 0x8080 + p lies in [2^23, 2^24), where the float's ulp is 1, so
-            // its mantissa bits are q = p + 0x8080 and p = (q2 << 16) + ((q1 -
-            // 128) << 8) + (q0 - 128) with q's bytes q2 (0 .. 32) and q1, q0:
-            // the digits are byte 2 and bytes 1, 0 xor 0x80 (int8).
+            // p = w * v_scale rounded to an integer (0 <= p < 2^23 - 2^16): t =
+            // 2^23 + 0x8080 + p lies in [2^23, 2^24), where the float's ulp is
+            // 1, so its mantissa bits are q = p + 0x8080 and p = (q2 << 16) +
+            // ((q1 - 128) << 8) + (q0 - 128) with q's bytes q2 (0 .. 127) and
+            // q1, q0: the digits are byte 2 and bytes 1, 0 xor 0x80 (int8).
             x[e] = __float_as_uint(fmaf(w, vsl, 8421504.f));
           }
           // 4 x 3 byte transpose: digit k of the four tokens into one word.
@@ -1113,34 +1151,42 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
       };
       if (vfull) weights(std::false_type{});
       else weights(std::true_type{});
-      const float inv = __builtin_amdgcn_ldexpf(1.f, -kp);
-      l_run = fmaf(lw, inv, l_run * f);
+      l_run = fmaf(lw, __builtin_amdgcn_ldexpf(1.f, -kp), l_run);
       uint8_t* const xb = smem + kXBase + (blk * 2u + (t & 1u)) * kXBytes;
   #pragma unroll
       for (int dg = 0; dg < 3; ++dg) *reinterpret_cast<i32x4*>(xb + 1024u * dg + 16u * lane) = bd[dg];
-      if (g == 0) fx_s[blk][t & 1u][n] = f;
-      if (lane == 0) fx_s[blk][t & 1u][16] = inv;
     };
 
-    auto write_ml = [&](uint32_t sp) __attribute__((always_inline)) {
-      const float l_h = rows_sum(l_run);
+    // A split's end (after its tile t): the partial relative to the true
+    // maximum, e = 2^(R - m) (1 .. 2^kPcHeadroom), also for the PV waves.
+    auto write_ml = [&](uint32_t sp, uint32_t t) __attribute__((always_inline)) {
+      const float e = m_run == neg_inf() ? 0.f : __builtin_amdgcn_exp2f(R - m_run);
+      const float l_h = rows_sum(l_run) * e;
       if (hvalid && g == 0) {
         float* const dst = partial(sp);
         dst[0] = m_run * kLn2;
         dst[1] = l_h;
       }
+      if (t != ~0u) {
+        float* const fx = fx_s[blk][t & 1u];
+        if (g == 0) fx[18 + n] = e;
+        if (lane == 0) fx[34] = epoch ? __builtin_amdgcn_ldexpf(1.f, -kp) : 0.f;
+      }
       m_run = neg_inf();
       l_run = 0.f;
+      R = neg_inf();
+      epoch = false;
+      epoch_tiles = 0;
     };
     for (uint32_t s = 0; s <= ntiles; ++s) {
       __syncthreads();
       if (has && s < ntiles) {
         if (s < nvis) qk_tile(s);
-        if (s % tps == tps - 1u || s + 1u == ntiles) write_ml(sp0 + s / tps);
+        if (s % tps == tps - 1u || s + 1u == ntiles) write_ml(sp0 + s / tps, s);
       }
     }
     if (has)
-      for (uint32_t sp = sp_e; sp < sp1; ++sp) write_ml(sp);
+      for (uint32_t sp = sp_e; sp < sp1; ++sp) write_ml(sp, ~0u);
     return;
   }
   // PV waves: wave 4 + j takes the 16-dim blocks 4j .. 4j + 3 of every
@@ -1149,76 +1195,68 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
   const uint32_t pj = wave - 4u;
   bare_barrier();  // the prologue barrier (see the DMA wave)
   f32x4 acc[kPcBlocks][4];  // [block][m]: lane (h, g): dims 16 (4j + m) + 4g + e
+  i32x4 cv[kPcBlocks][4][3];  // the current epoch's digit sums, digit 0 (top) .. 2
 #pragma unroll
   for (uint32_t b = 0; b < kPcBlocks; ++b)
 #pragma unroll
-    for (int m = 0; m < 4; ++m) acc[b][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < 4; ++m) {
+      acc[b][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int dg = 0; dg < 3; ++dg) cv[b][m][dg] = i32x4{0, 0, 0, 0};
+    }
+  // An epoch's digit sums into fp32: acc = (acc + (V . P) * 2^-kp) * f.
+  auto fold = [&](auto bc, float f, float inv) __attribute__((always_inline)) {
+    constexpr uint32_t b = decltype(bc)::value;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = fmaf(float(cv[b][m][0][e]), 65536.f, fmaf(float(cv[b][m][1][e]), 256.f, float(cv[b][m][2][e])));
+        acc[b][m][e] = fmaf(x, inv, acc[b][m][e]) * f;
+      }
+#pragma unroll
+      for (int dg = 0; dg < 3; ++dg) cv[b][m][dg] = i32x4{0, 0, 0, 0};
+    }
+  };
   auto pv_tile = [&](uint32_t t) __attribute__((always_inline)) {
     const uint32_t va = lds_base + (t % kPcSlots) * kImg + voff + 4096u * pj;
     const uint32_t xs = t & 1u;
-    // A block this tile does not reach (past its visible range, or absent)
-    // gets zero digits, f = 1 and 2^-kp = 0, so its numerators stay as they
-    // are and the pipeline has no branch.
-    i32x4 bd[kPcBlocks][3];
-    float f[kPcBlocks], inv[kPcBlocks];
-#pragma unroll
-    for (uint32_t b = 0; b < kPcBlocks; ++b) {
-      const bool live = b < hblocks && t < nvis_s[b];
-      const uint8_t* const xb = smem + kXBase + (b * 2u + xs) * kXBytes;
-#pragma unroll
-      for (int dg = 0; dg < 3; ++dg)
-        bd[b][dg] = live ? *reinterpret_cast<const i32x4*>(xb + 1024u * dg + 16u * lane) : i32x4{0, 0, 0, 0};
-      f[b] = live ? fx_s[b][xs][n] : 1.f;
-      inv[b] = live ? fx_s[b][xs][16] : 0.f;
-    }
-#pragma unroll
-    for (uint32_t b = 0; b < kPcBlocks; ++b)
-      if (__builtin_amdgcn_ballot_w64(f[b] != 1.f) != 0u)  // skipped where no maximum of the block rose
-#pragma unroll
-        for (int m = 0; m < 4; ++m) acc[b][m] *= f[b];
     u32x4_t vr[4];
     ds_issue16x1<0u>(va, vr[0]);
     ds_issue16x1<1024u>(va, vr[1]);
     ds_issue16x1<2048u>(va, vr[2]);
     ds_issue16x1<3072u>(va, vr[3]);
-    i32x4 cv[2][3];
-    // unit u: dim block m = u / 3 of head-row block b = u % 3; its MFMAs
-    // run with the previous unit's fold
-    auto fold = [&](auto uc) __attribute__((always_inline)) {
-      constexpr uint32_t u = decltype(uc)::value, m = u / 3u, b = u % 3u;
-      const i32x4(&cc)[3] = cv[u & 1u];
+    wait_lgkm<0>();
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int hi2 = cc[0][e] * 256 + cc[1][e];  // digits in base 256: |.| < 2^27
-        acc[b][m][e] = fmaf(fmaf(float(hi2), 256.f, float(cc[2][e])), inv[b], acc[b][m][e]);
-      }
-    };
-    static_for<0, 12>([&](auto uc) __attribute__((always_inline)) {
-      constexpr uint32_t u = decltype(uc)::value, m = u / 3u, b = u % 3u;
-      if constexpr (b == 0u) {
-        wait_lgkm<3u - m>();  // dim block m's V rows landed; the later ones may be in flight
-        pin(vr[m]);
-      }
-      i32x4(&cc)[3] = cv[u & 1u];
-      const i32x4 av = {int(vr[m][0]), int(vr[m][1]), int(vr[m][2]), int(vr[m][3])};
+    for (int m = 0; m < 4; ++m) pin(vr[m]);
+    static_for<0, kPcBlocks>([&](auto bc) __attribute__((always_inline)) {
+      constexpr uint32_t b = decltype(bc)::value;
+      if (b >= hblocks || t >= nvis_s[b]) return;  // a block this tile does not reach
+      const float* const fx = fx_s[b][xs];
+      if (fx[17] != 0.f) fold(bc, fx[n], fx[16]);  // the tile starts a new epoch
+      const uint8_t* const xb = smem + kXBase + (b * 2u + xs) * kXBytes;
+      i32x4 bd[3];
 #pragma unroll
-      for (int dg = 0; dg < 3; ++dg) cc[dg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bd[b][dg], i32x4{0, 0, 0, 0}, 0, 0, 0);
-      if constexpr (u > 0) {
-        fold(std::integral_constant<uint32_t, u - 1>{});
+      for (int dg = 0; dg < 3; ++dg) bd[dg] = *reinterpret_cast<const i32x4*>(xb + 1024u * dg + 16u * lane);
 #pragma unroll
-        for (int i = 0; i < 3; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // then up to four VALU
-        }
+      for (int m = 0; m < 4; ++m) {
+        const i32x4 av = {int(vr[m][0]), int(vr[m][1]), int(vr[m][2]), int(vr[m][3])};
+#pragma unroll
+        for (int dg = 0; dg < 3; ++dg) cv[b][m][dg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bd[dg], cv[b][m][dg], 0, 0, 0);
       }
     });
-    fold(std::integral_constant<uint32_t, 11>{});
   };
 
-  auto write_n = [&](uint32_t sp) __attribute__((always_inline)) {
-#pragma unroll
-    for (uint32_t b = 0; b < kPcBlocks; ++b) {
+  // A split's end (after its tile t): fold the last epoch, scale to the true
+  // maximum (e), write, restart.
+  auto write_n = [&](uint32_t sp, uint32_t t) __attribute__((always_inline)) {
+    static_for<0, kPcBlocks>([&](auto bc) __attribute__((always_inline)) {
+      constexpr uint32_t b = decltype(bc)::value;
       const uint32_t hrb = b * 16u + n;
+      if (b < hblocks && t != ~0u) {
+        const float* const fx = fx_s[b][t & 1u];
+        fold(bc, fx[18 + n], fx[34]);
+      }
       if (b < hblocks && hrb < head_rows) {
         const uint32_t rowb = hrb / a.group, headb = kv * a.group + hrb % a.group;
         float* const dst = scratch + ((size_t(rowb) * a.q_heads + headb) * a.splits + sp) * W + 2 + 64u * pj;
@@ -1229,7 +1267,7 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
       }
 #pragma unroll
       for (int m = 0; m < 4; ++m) acc[b][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    });
   };
 
   for (uint32_t s = 0; s <= ntiles; ++s) {
@@ -1237,10 +1275,10 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
     if (s > 0u) {
       const uint32_t t = s - 1u;
       pv_tile(t);
-      if (t % tps == tps - 1u || t + 1u == ntiles) write_n(sp0 + t / tps);
+      if (t % tps == tps - 1u || t + 1u == ntiles) write_n(sp0 + t / tps, t);
     }
   }
-  for (uint32_t sp = sp_e; sp < sp1; ++sp) write_n(sp);
+  for (uint32_t sp = sp_e; sp < sp1; ++sp) write_n(sp, ~0u);
 }
 
 #define KVB_I8R_ARGS                                                                             \
