@@ -851,7 +851,6 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
   }
   const uint32_t voff = G::kKBytes + 64u * n + 16u * (g ^ swz_v(n));
   const uint32_t soff = G::kKBytes + G::kVBytes + 64u * g;
-  const uint32_t vmoff = G::kKBytes + G::kVBytes + 256u + 4u * lane;
 
   const uint32_t hr = blk * 16u + n;
   const bool hvalid = has && hr < head_rows;
@@ -1007,7 +1006,7 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
       uint32_t ka[KS];
   #pragma unroll
       for (int s = 0; s < KS; ++s) ka[s] = pb + koff[s];
-      const uint32_t sa = pb + soff, vma = pb + vmoff;
+      const uint32_t sa = pb + soff;
       const uint32_t t0 = (k_first + t) * kTileTokens;
       float sc[16];
       float mx = neg_inf();
@@ -1076,11 +1075,64 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
       else qk(std::true_type{});
       pin(mx);
 
-      // v-scales of the tile (lane = token), running maximum, weight exponent kp.
-      const float v = __uint_as_float(ds_read4_sync<0>(vma));
-      const float vm = t0 + lane < e_max ? fabsf(v) : 0.f;
+      // v-scales of tokens 16g .. 16g + 15 (zero past the block's last
+      // visible token, so stale LDS contents cannot reach the digits).
+      const uint32_t vlim = e_max > t0 ? (e_max - t0 < kTileTokens ? e_max - t0 : kTileTokens) : 0u;
+      float vsl[16];
+      {
+        u32x4_t vsr[4];
+        ds_read16x4<256u, 272u, 288u, 304u>(sa, vsr[0], vsr[1], vsr[2], vsr[3]);
+  #pragma unroll
+        for (int i = 0; i < 16; ++i) vsl[i] = __uint_as_float(vsr[i / 4][i % 4]);
+        if (t0 + kTileTokens > e_max) {
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) vsl[i] = 16u * g + i < vlim ? vsl[i] : 0.f;
+        }
+      }
+      float vloc = 0.f;
+  #pragma unroll
+      for (int i = 0; i < 16; ++i) vloc = fmaxf(vloc, fabsf(vsl[i]));
+
+      // Weights as three base-256 int8 digits (k-position = token 16g + 4mb + e).
+      i32x4 bd[3];
+      float lw = 0.f;
+      auto weights = [&](float mu) __attribute__((always_inline)) {  // 2^(s - mu) = w * 2^kp
+        lw = 0.f;
+        uint32_t bw[3][4];
+  #pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          uint32_t x[4];
+  #pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float w = __builtin_amdgcn_exp2f(fmaf(sc[4 * mb + e], cs, -mu));  // w * 2^kp
+            lw += w;
+            // p = w * v_scale rounded to an integer (0 <= p < 2^23 - 2^16): t =
+            // 2^23 + 0x8080 + p lies in [2^23, 2^24), where the float's ulp is
+            // 1, so its mantissa bits are q = p + 0x8080 and p = (q2 << 16) +
+            // ((q1 - 128) << 8) + (q0 - 128) with q's bytes q2 (0 .. 127) and
+            // q1, q0: the digits are byte 2 and bytes 1, 0 xor 0x80 (int8).
+            x[e] = __float_as_uint(fmaf(w, vsl[4 * mb + e], 8421504.f));
+          }
+          // 4 x 3 byte transpose: digit k of the four tokens into one word.
+          const uint32_t lo01 = __builtin_amdgcn_perm(x[1], x[0], 0x05010400u);  // x0.b0 x1.b0 x0.b1 x1.b1
+          const uint32_t lo23 = __builtin_amdgcn_perm(x[3], x[2], 0x05010400u);
+          const uint32_t hi01 = __builtin_amdgcn_perm(x[1], x[0], 0x0c0c0602u);  // x0.b2 x1.b2 0 0
+          const uint32_t hi23 = __builtin_amdgcn_perm(x[3], x[2], 0x06020c0cu);  // 0 0 x2.b2 x3.b2
+          bw[0][mb] = hi01 | hi23;
+          bw[1][mb] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
+          bw[2][mb] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
+        }
+  #pragma unroll
+        for (int dg = 0; dg < 3; ++dg) bd[dg] = i32x4{int(bw[dg][0]), int(bw[dg][1]), int(bw[dg][2]), int(bw[dg][3])};
+      };
+      // The epoch's reference first (right unless this tile starts a new
+      // epoch), so the weights need not wait for the cross-lane maxima.
+      weights((R == neg_inf() ? 0.f : R) - float(kp));
+
+      // Running maximum and the tile's largest v-scale; a new epoch redoes
+      // the weights.
       const float m_new = fmaxf(m_run, rows_max(mx) * cs);
-      const float vmax = wave_max(vm);
+      const float vmax = rows_max(vloc);
       float* const fx = fx_s[blk][t & 1u];
       const bool rise = __builtin_amdgcn_ballot_w64(m_new > R) != 0u;
       if (!epoch || rise || vmax >= vcap || vmax < vlo || epoch_tiles >= 1024u) {
@@ -1103,54 +1155,12 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
         vlo = 0.25f * vmax;
         epoch_tiles = 0;
         epoch = true;
+        weights((R == neg_inf() ? 0.f : R) - float(kp));
       } else if (lane == 0) {
         fx[17] = 0.f;
       }
       ++epoch_tiles;
       m_run = m_new;
-      const float mu = (R == neg_inf() ? 0.f : R) - float(kp);  // 2^(s - mu) = w * 2^kp, w <= 1
-
-      // Weights as three base-256 int8 digits (k-position = token 16g + 4mb +
-      // e); slots past the block's last visible token get a zero v-scale.
-      const uint32_t vlim = e_max > t0 ? (e_max - t0 < kTileTokens ? e_max - t0 : kTileTokens) : 0u;
-      const bool vfull = t0 + kTileTokens <= e_max;
-      i32x4 bd[3];
-      float lw = 0.f;
-      auto weights = [&](auto maskc) __attribute__((always_inline)) {
-        constexpr bool MASK = decltype(maskc)::value;
-        u32x4_t vsr[4];  // v-scales of tokens 16g .. 16g + 15
-        ds_read16x4<256u, 272u, 288u, 304u>(sa, vsr[0], vsr[1], vsr[2], vsr[3]);
-        uint32_t bw[3][4];
-  #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          uint32_t x[4];
-  #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float w = __builtin_amdgcn_exp2f(fmaf(sc[4 * mb + e], cs, -mu));  // w * 2^kp
-            lw += w;
-            float vsl = __uint_as_float(vsr[mb][e]);
-            if constexpr (MASK) vsl = 16u * g + 4u * mb + e < vlim ? vsl : 0.f;
-            // p = w * v_scale rounded to an integer (0 <= p < 2^23 - 2^16): t =
-            // 2^23 + 0x8080 + p lies in [2^23, 2^24), where the float's ulp is
-            // 1, so its mantissa bits are q = p + 0x8080 and p = (q2 << 16) +
-            // ((q1 - 128) << 8) + (q0 - 128) with q's bytes q2 (0 .. 127) and
-            // q1, q0: the digits are byte 2 and bytes 1, 0 xor 0x80 (int8).
-            x[e] = __float_as_uint(fmaf(w, vsl, 8421504.f));
-          }
-          // 4 x 3 byte transpose: digit k of the four tokens into one word.
-          const uint32_t lo01 = __builtin_amdgcn_perm(x[1], x[0], 0x05010400u);  // x0.b0 x1.b0 x0.b1 x1.b1
-          const uint32_t lo23 = __builtin_amdgcn_perm(x[3], x[2], 0x05010400u);
-          const uint32_t hi01 = __builtin_amdgcn_perm(x[1], x[0], 0x0c0c0602u);  // x0.b2 x1.b2 0 0
-          const uint32_t hi23 = __builtin_amdgcn_perm(x[3], x[2], 0x06020c0cu);  // 0 0 x2.b2 x3.b2
-          bw[0][mb] = hi01 | hi23;
-          bw[1][mb] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
-          bw[2][mb] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
-        }
-  #pragma unroll
-        for (int dg = 0; dg < 3; ++dg) bd[dg] = i32x4{int(bw[dg][0]), int(bw[dg][1]), int(bw[dg][2]), int(bw[dg][3])};
-      };
-      if (vfull) weights(std::false_type{});
-      else weights(std::true_type{});
       l_run = fmaf(lw, __builtin_amdgcn_ldexpf(1.f, -kp), l_run);
       uint8_t* const xb = smem + kXBase + (blk * 2u + (t & 1u)) * kXBytes;
   #pragma unroll
