@@ -76,6 +76,7 @@ hipError_t launch_split_generic(const SplitArgs& a, bool int8, hipStream_t strea
 const char* lds_kernel_name(const SplitArgs& a);
 const char* i8_kernel_name(const SplitArgs& a);
 const char* split_kernel_name(const SplitArgs& a, bool tiled, bool int8);
+uint32_t device_cus();  // compute units of the current device (cached per device)
 // out_type: 0 none, 1 fp32, 2 fp16 (kvbridge_c.h KVB_OUT_*).
 hipError_t launch_merge(uint32_t row_heads, uint32_t dim, uint32_t splits, const float* scratch,
                         float* m, float* l, float* n, void* out, int out_type,

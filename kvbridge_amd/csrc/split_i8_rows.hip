@@ -781,6 +781,7 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
   // 18-33, 2^-kp of its last epoch at 34)
   __shared__ float fx_s[kPcBlocks][2][36];
   __shared__ uint32_t nvis_s[kPcBlocks];
+  __shared__ uint32_t rh_s[kPcBlocks * 16u];  // row * q_heads + head of each head-row (partial offsets)
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t n = lane & 15u, g = lane >> 4;
@@ -983,6 +984,7 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
       cs = cs >= 1.17549435e-38f ? cs : 1.17549435e-38f;
       nvis = e_max > s0 ? (e_max - 1u) / kTileTokens + 1u - k_first : 0u;
       if (lane == 0) nvis_s[blk] = nvis;
+      if (g == 0) rh_s[hr] = row * a.q_heads + head;
     }
 
     float m_run = neg_inf(), l_run = 0.f;  // head-row h's running max (log2) and partial sum
@@ -1126,8 +1128,9 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
         for (int dg = 0; dg < 3; ++dg) bd[dg] = i32x4{int(bw[dg][0]), int(bw[dg][1]), int(bw[dg][2]), int(bw[dg][3])};
       };
       // The epoch's reference first (right unless this tile starts a new
-      // epoch), so the weights need not wait for the cross-lane maxima.
-      weights((R == neg_inf() ? 0.f : R) - float(kp));
+      // epoch), so the weights need not wait for the cross-lane maxima.  A
+      // split's first tile always starts one.
+      if (epoch) weights((R == neg_inf() ? 0.f : R) - float(kp));
 
       // Running maximum and the tile's largest v-scale; a new epoch redoes
       // the weights.
@@ -1243,7 +1246,9 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
       constexpr uint32_t b = decltype(bc)::value;
       if (b >= hblocks || t >= nvis_s[b]) return;  // a block this tile does not reach
       const float* const fx = fx_s[b][xs];
-      if (fx[17] != 0.f) fold(bc, fx[n], fx[16]);  // the tile starts a new epoch
+      // The tile starts a new epoch: fold the one that ends (none at a
+      // split's first epoch, whose accumulators are still zero).
+      if (fx[17] != 0.f && fx[16] != 0.f) fold(bc, fx[n], fx[16]);
       const uint8_t* const xb = smem + kXBase + (b * 2u + xs) * kXBytes;
       i32x4 bd[3];
 #pragma unroll
@@ -1268,8 +1273,7 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
         fold(bc, fx[18 + n], fx[34]);
       }
       if (b < hblocks && hrb < head_rows) {
-        const uint32_t rowb = hrb / a.group, headb = kv * a.group + hrb % a.group;
-        float* const dst = scratch + ((size_t(rowb) * a.q_heads + headb) * a.splits + sp) * W + 2 + 64u * pj;
+        float* const dst = scratch + (size_t(rh_s[hrb]) * a.splits + sp) * W + 2 + 64u * pj;
 #pragma unroll
         for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -1294,22 +1298,6 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
 #define KVB_I8R_ARGS                                                                             \
   a, a.q, a.q_positions, a.k_positions, a.page_table, static_cast<const int8_t*>(a.k),             \
       static_cast<const int8_t*>(a.v), a.k_scales, a.v_scales, a.scratch, spw
-
-// Compute units of the current device (cached per device; callers on
-// several threads may fill an entry concurrently with the same value).
-uint32_t device_cus() {
-  static std::atomic<uint32_t> cache[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256u;
-  uint32_t v = cache[dev].load(std::memory_order_relaxed);
-  if (v == 0u) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    v = uint32_t(n);
-    cache[dev].store(v, std::memory_order_relaxed);
-  }
-  return v;
-}
 
 // The wave-specialized kernel: dim 256 and one round of at most three
 // head-row blocks (17 to 48 head-rows).
@@ -1386,6 +1374,22 @@ hipError_t preload_i8_rows() {
   const hipError_t e = preload_dim<128>();
   if (e != hipSuccess) return e;
   return preload_dim<256>();
+}
+
+// Compute units of the current device (cached per device; callers on
+// several threads may fill an entry concurrently with the same value).
+uint32_t device_cus() {
+  static std::atomic<uint32_t> cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256u;
+  uint32_t v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0u) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    v = uint32_t(n);
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
 }
 
 }  // namespace kvb
