@@ -119,7 +119,8 @@ __global__ __launch_bounds__(kSliceThreads) void merge_slices_kernel(
 #pragma unroll
     for (uint32_t k = 0; k < K; ++k) {
       const uint32_t j = j0 + g + G * k;
-      v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, int(((j < S ? j : S - 1u) * W + 2u + col) * 4u), 0, 0);
+      v[k] = merge_detail::u32x4{0u, 0u, 0u, 0u};  // splits past S: no load (not read below)
+      if (j < S) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, int((j * W + 2u + col) * 4u), 0, 0);
     }
     if (passes == 1u) M = block_max(mj);
     const float f = jt < S && lj > 0.f ? exp_e(mj - M) : 0.f;
