@@ -276,12 +276,16 @@ def test_split_size_invariance(gpu):
 
 
 MERGE_CASES = [
-    # dim, tokens (256-token splits), query position cut
+    # dim, tokens (256-token splits), query position cut, rows (x 8 q-heads = row-heads).
+    # Above 64 splits the merge runs on dim slices, as wide as still gives two
+    # work-groups per CU (on 256 CUs: 16 dims below 128 row-heads at dim 128).
     (128, 3000, None, 2),       # 12 splits: merge_rows, one pass
-    (256, 100 * 256, None, 1),  # 100 splits: the wide merge, one pass
-    (256, 600 * 256, 0.5, 1),   # 600 splits: wide, three passes, the later half empty (m = -inf, l = 0)
-    (128, 700 * 256, None, 1),  # wide, two passes
-    (64, 1100 * 256, 0.3, 1),   # wide, two passes, mostly empty
+    (256, 100 * 256, None, 1),  # 100 splits: 16-dim slices, one pass
+    (256, 600 * 256, 0.5, 1),   # 600 splits: three passes, the later half empty (m = -inf, l = 0)
+    (128, 700 * 256, None, 1),  # two passes
+    (64, 1100 * 256, 0.3, 1),   # two passes, mostly empty
+    (128, 150 * 256, None, 20),  # 160 row-heads: 32-dim slices
+    (256, 70 * 256, 0.6, 64),    # 512 row-heads: 64-dim slices, the last splits empty
 ]
 
 
