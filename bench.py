@@ -594,6 +594,20 @@ def main():
             mma[key] = rec
             log(f"mma geometry ({key}, {nspl} splits): {mus:.2f} us ({gbs(mbytes, mus):.0f} GB/s, "
                 f"{rec['pct_of_peak']:.1f}% of peak)")
+        if args.mma_calls == "both":
+            # The same K, V and scale bytes through the same page table (two
+            # 32-token pages per 64-token tile) with the 1,024-token work split
+            # and no arithmetic: the read floor of this access pattern.
+            msink = torch.zeros(kvb.split_count(ms_, dst_) * ms_.kv_heads, dtype=torch.int32, device=dev)
+            pus = warm_and_time(lambda i: kvb.paged_read_probe(ms_, minps[i % copies], dst_, msink, sp),
+                                steps=max(50, args.steps // 4), warmup=10) * 1e3
+            mma["paged_probe_1024_token_splits"] = {
+                "us": round(pus, 3), "GB/s": round(gbs(mbytes, pus), 1),
+                "pct_of_peak": round(100.0 * gbs(mbytes, pus) / HBM_PEAK_GBS, 2),
+                "note": "the geometry's own K, V and scale bytes through its page table, 1024-token work split, "
+                        "no arithmetic (kvb_paged_read_probe)"}
+            log(f"mma geometry paged probe (1024-token splits): {pus:.2f} us ({gbs(mbytes, pus):.0f} GB/s, "
+                f"{mma['paged_probe_1024_token_splits']['pct_of_peak']:.1f}% of peak)")
         del mcaches, minps, msc
         torch.cuda.empty_cache()
 

@@ -242,9 +242,10 @@ int kvb_hbm_read_probe(const void* src, size_t bytes, uint32_t* sink, uint32_t b
  * page table and with the decode kernels' work split (one work-group of 8
  * waves per split and kv head, 64-token tiles round-robin over the waves),
  * and computes nothing: the read floor of the paged access pattern next to
- * the attention kernels.  Needs int8 KV, dim 64/128/256, page_tokens,
- * split_tokens and begin multiples of 64, 16-byte aligned K/V.  `sink` needs
- * splits * kv_heads uint32 and is practically never written. */
+ * the attention kernels.  Needs int8 KV, dim 64/128/256, page_tokens 16, 32
+ * or a multiple of 64, split_tokens and begin multiples of 64, 16-byte
+ * aligned K/V.  `sink` needs splits * kv_heads uint32 and is practically
+ * never written. */
 int kvb_paged_read_probe(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens, uint32_t* sink,
                          void* stream);
 

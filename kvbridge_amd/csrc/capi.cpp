@@ -461,10 +461,11 @@ int kvb_paged_read_probe(const kvb_shape* sp, const kvb_device_input* ip, uint32
     const kvbridge::DeviceInput in = to_input(*ip);
     if (const char* e = launch_error(s, in, sink)) return fail(KVB_EINVAL, e);
     const auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-    if (!s.int8 || (s.dim != 64 && s.dim != 128 && s.dim != 256) || s.page_tokens % 64 != 0 || split_tokens % 64 != 0 ||
+    if (!s.int8 || (s.dim != 64 && s.dim != 128 && s.dim != 256) || (s.page_tokens % 64 != 0 && s.page_tokens != 16 && s.page_tokens != 32) || split_tokens % 64 != 0 ||
         s.begin % 64 != 0 || !al16(in.k) || !al16(in.v))
       return fail(KVB_EINVAL,
-                  "paged probe needs int8 KV, dim 64/128/256, 64-token-aligned pages, splits and begin, "
+                  "paged probe needs int8 KV, dim 64/128/256, pages of 16, 32 or a multiple of 64 tokens, "
+                  "64-token-aligned splits and begin, "
                   "16-byte aligned K/V");
     const unsigned splits = kvbridge::split_count(s, split_tokens);
     return hip_status(kvb::launch_paged_read_probe(in.page_table, in.k, in.v, in.k_scales, in.v_scales, s.kv_heads,

@@ -50,8 +50,10 @@ __global__ __launch_bounds__(kThreads) void read_probe_kernel(const u32x4* __res
 // 64-token tiles w, w + 8, ... of its split; per tile the K rows (64 x dim
 // contiguous bytes), the V rows (dim rows of 64 bytes, stride page_tokens)
 // and the 64 k- and v-scales are requested together, one tile in flight per
-// wave.  Tiles lie in one page (page_tokens a multiple of 64).
-template <int D>
+// wave.  A tile lies in one page (page_tokens a multiple of 64) or, with
+// SUB, spans 64 / page_tokens pages (page_tokens 16 or 32), whose table
+// entries the wave reads at the tile's start.
+template <int D, bool SUB>
 __global__ __launch_bounds__(kThreads) void paged_read_probe_kernel(
     const uint32_t* __restrict__ table, const int8_t* __restrict__ k, const int8_t* __restrict__ v,
     const uint32_t* __restrict__ ks, const uint32_t* __restrict__ vs, uint32_t kv_heads, uint32_t page_tokens,
@@ -62,7 +64,58 @@ __global__ __launch_bounds__(kThreads) void paged_read_probe_kernel(
   const uint32_t s0 = begin + split * split_tokens;
   const uint32_t s1 = s0 + split_tokens < end ? s0 + split_tokens : end;
   uint32_t acc = 0;
-  for (uint32_t t0 = s0 + 64u * wave; t0 < s1; t0 += 64u * kWaves) {
+  const uint32_t lpages = (end + page_tokens - 1u) / page_tokens;  // logical pages of the sequence
+  constexpr uint32_t NP = SUB ? 4u : 1u;  // pages a tile can span (16-token pages)
+  for (uint32_t t0 = s0 + 64u * wave; t0 < s1 && SUB; t0 += 64u * kWaves) {
+    // The tile's pages (wave-uniform: one table entry per page, not per
+    // lane); a tile may run past `end`: clamp to the last logical page,
+    // whose bytes the tile's own pages hold anyway.
+    uint32_t pg[NP];
+#pragma unroll
+    for (uint32_t i = 0; i < NP; ++i) {
+      pg[i] = 0u;
+      if (i * page_tokens >= 64u) continue;  // past the tile
+      uint32_t lp = t0 / page_tokens + i;
+      lp = lp < lpages ? lp : lpages - 1u;
+      const uint32_t page = table[lp];
+      pg[i] = page < pages ? page : pages - 1u;
+    }
+    // Physical slab and slot of token t of the tile.
+    auto at = [&](uint32_t t, size_t& slab, uint32_t& slot) __attribute__((always_inline)) {
+      const uint32_t i = (t - t0) / page_tokens;
+      uint32_t page = pg[0];
+#pragma unroll
+      for (uint32_t x = 1; x < NP; ++x) page = i == x ? pg[x] : page;
+      slab = size_t(page) * kv_heads + kv;
+      slot = t % page_tokens;
+    };
+    u32x4 kx[kPieces], vx[kPieces];
+#pragma unroll
+    for (uint32_t j = 0; j < kPieces; ++j) {
+      const uint32_t byte = 16u * (64u * j + lane);
+      size_t slab;
+      uint32_t slot;
+      at(t0 + byte / D, slab, slot);
+      kx[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(k + (slab * page_tokens + slot) * D + byte % D));
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kPieces; ++j) {
+      const uint32_t piece = 64u * j + lane, row = piece >> 2, seg = piece & 3u;
+      size_t slab;
+      uint32_t slot;
+      at(t0 + 16u * seg, slab, slot);
+      vx[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(v + (slab * D + row) * page_tokens + slot));
+    }
+    size_t slab;
+    uint32_t slot;
+    at(t0 + lane, slab, slot);
+    const uint32_t a = __builtin_nontemporal_load(ks + slab * page_tokens + slot);
+    const uint32_t b = __builtin_nontemporal_load(vs + slab * page_tokens + slot);
+    acc ^= a ^ b;
+#pragma unroll
+    for (uint32_t j = 0; j < kPieces; ++j) acc ^= kx[j][0] ^ kx[j][1] ^ kx[j][2] ^ kx[j][3] ^ vx[j][0] ^ vx[j][1] ^ vx[j][2] ^ vx[j][3];
+  }
+  for (uint32_t t0 = s0 + 64u * wave; t0 < s1 && !SUB; t0 += 64u * kWaves) {
     uint32_t page = table[t0 / page_tokens];
     page = page < pages ? page : pages - 1u;
     const size_t slab = size_t(page) * kv_heads + kv;
@@ -97,22 +150,21 @@ hipError_t launch_paged_read_probe(const uint32_t* table, const void* k, const v
   const auto* v8 = static_cast<const int8_t*>(v);
   const auto* ks32 = reinterpret_cast<const uint32_t*>(ks);
   const auto* vs32 = reinterpret_cast<const uint32_t*>(vs);
+  const bool sub = page_tokens < 64u;
+#define KVB_PROBE(DD)                                                                                            \
+  if (sub)                                                                                                       \
+    hipLaunchKernelGGL((paged_read_probe_kernel<DD, true>), grid, dim3(kThreads), 0, stream, table, k8, v8, ks32, \
+                       vs32, kv_heads, page_tokens, pages, begin, end, split_tokens, sink);                      \
+  else                                                                                                           \
+    hipLaunchKernelGGL((paged_read_probe_kernel<DD, false>), grid, dim3(kThreads), 0, stream, table, k8, v8,     \
+                       ks32, vs32, kv_heads, page_tokens, pages, begin, end, split_tokens, sink);
   switch (dim) {
-    case 64:
-      hipLaunchKernelGGL(paged_read_probe_kernel<64>, grid, dim3(kThreads), 0, stream, table, k8, v8, ks32, vs32,
-                         kv_heads, page_tokens, pages, begin, end, split_tokens, sink);
-      break;
-    case 128:
-      hipLaunchKernelGGL(paged_read_probe_kernel<128>, grid, dim3(kThreads), 0, stream, table, k8, v8, ks32, vs32,
-                         kv_heads, page_tokens, pages, begin, end, split_tokens, sink);
-      break;
-    case 256:
-      hipLaunchKernelGGL(paged_read_probe_kernel<256>, grid, dim3(kThreads), 0, stream, table, k8, v8, ks32, vs32,
-                         kv_heads, page_tokens, pages, begin, end, split_tokens, sink);
-      break;
-    default:
-      return hipErrorInvalidValue;
+    case 64: KVB_PROBE(64) break;
+    case 128: KVB_PROBE(128) break;
+    case 256: KVB_PROBE(256) break;
+    default: return hipErrorInvalidValue;
   }
+#undef KVB_PROBE
   return hipGetLastError();
 }
 
