@@ -209,12 +209,13 @@ int kvb_append_kv(const kvb_append_shape* s, const kvb_append_io* io, void* stre
  * loops, harnesses that forbid hipMalloc): kvb_decode_attention_fused with its
  * scratch -- the split partials and the merge counters -- taken from a fixed
  * 8 MiB device array inside the library instead of caller buffers.  Same
- * kernels, results bitwise equal to kvb_decode_attention_fused.  A call whose
- * kv_heads counters (rounded up to 64) plus kvb_scratch_elements_ex floats
- * exceed 8 MiB is rejected with KVB_EINVAL.  The array is per device and
- * shared by every call on that device, which leaves the counters zero and the
- * partials as they were: calls that overlap on one device (several streams or
- * host threads) race.  Allocates nothing. */
+ * kernels, results bitwise equal to kvb_decode_attention_fused.  The array
+ * holds a fixed region of 512 counter words (the most a single launch uses)
+ * and then the partials; a call whose kvb_scratch_elements_ex floats exceed
+ * the remaining 8 MiB - 2 KiB is rejected with KVB_EINVAL.  The array is per
+ * device and shared by every call on that device, which leaves the counters
+ * zero and the partials as they were: calls that overlap on one device
+ * (several streams or host threads) race.  Allocates nothing. */
 int kvb_decode_attention_noalloc(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens, float* m,
                                  float* l, float* n, void* out, int out_type, void* stream);
 

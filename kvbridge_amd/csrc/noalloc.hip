@@ -8,9 +8,14 @@
 // Host code never uses the array's name as a device address: the first call
 // on each device (with that device current) looks its address up with
 // hipGetSymbolAddress, and every call passes that pointer to the kernels.
-// The array is zero when the code object is loaded, and every completed call
-// leaves its counter words zero again (the merging work-group resets them),
-// which is the state the next call needs; partial words need no clearing.
+// Layout: a fixed counter region of kCounterWords words (one per kv head of
+// the largest single-launch grid: splits * kv_heads <= 512, so at most 512
+// kv heads), then the partials.  The region does not depend on the call's
+// kv_heads, so no call's partials ever land on another call's counter
+// words.  The array is zero when the code object is loaded, and every
+// completed single-launch call leaves the counter words it used zero again
+// (the merging work-group resets them), which is the state the next call
+// needs; partial words need no clearing.
 // Every call on one device shares that device's array: calls that overlap on
 // one device (two streams, two host threads) race.
 #include <hip/hip_runtime.h>
@@ -26,6 +31,7 @@ namespace {
 
 constexpr size_t kNoAllocBytes = size_t(8) << 20;       // 8 MiB per device
 constexpr size_t kNoAllocWords = kNoAllocBytes / 4;
+constexpr size_t kCounterWords = 512;  // = the single-launch grid limit (kv heads <= 512)
 constexpr uint32_t kMaxDevices = 64;
 
 static __device__ __align__(256) uint32_t scratch[kNoAllocWords];
@@ -60,19 +66,19 @@ int kvb_decode_attention_noalloc(const kvb_shape* sp, const kvb_device_input* ip
     return kvb_decode_attention_fused(sp, ip, split_tokens, nullptr, nullptr, m, l, n, out, out_type, stream);
   size_t partials = 0;
   if (const int rc = kvb_scratch_elements_ex(sp, split_tokens, &partials); rc != KVB_OK) return rc;
-  // Counter words first (one per kv head, rounded up to 256 bytes), then the
-  // partials.
-  const size_t counter_words = (size_t(sp->kv_heads) + 63u) / 64u * 64u;
-  if (counter_words + partials > kNoAllocWords)
+  // The fixed counter region first, then the partials.  A call that is not
+  // run as a single launch (more than 512 kv heads x splits) uses no counter,
+  // so kCounterWords covers every counter a call can touch.
+  if (partials > kNoAllocWords - kCounterWords)
     return kvb::set_error(KVB_EINVAL, "kvb_decode_attention_noalloc: the call needs " +
-                                          std::to_string((counter_words + partials) * 4) +
-                                          " bytes of scratch, the static area holds " + std::to_string(kNoAllocBytes) +
+                                          std::to_string(partials * 4) + " bytes of partials, the static area holds " +
+                                          std::to_string((kNoAllocWords - kCounterWords) * 4) +
                                           " (pass a buffer to kvb_decode_attention_fused instead)");
   void* base = nullptr;
   if (const hipError_t e = scratch_address(&base); e != hipSuccess)
     return kvb::set_error(KVB_ERUNTIME, std::string("no-alloc scratch lookup: ") + hipGetErrorString(e));
   uint32_t* counters = static_cast<uint32_t*>(base);
-  float* partial_base = reinterpret_cast<float*>(counters + counter_words);
+  float* partial_base = reinterpret_cast<float*>(counters + kCounterWords);
   return kvb_decode_attention_fused(sp, ip, split_tokens, partial_base, counters, m, l, n, out, out_type, stream);
 }
 

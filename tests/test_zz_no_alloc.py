@@ -57,3 +57,24 @@ def test_noalloc_rejects_oversized_call(gpu):
     inp = kvb.device_input(fake, fake, fake, fake, fake, fake, fake, fake)
     with pytest.raises(kvb.KvbInvalidArgument, match="static area"):
         kvb.decode_attention_noalloc(s, inp, 256, fake, fake, fake, fake, kvb.KVB_OUT_F16)
+
+
+def test_noalloc_kv_heads_across_counter_region(gpu):
+    # Calls on both sides of 64 kv heads in a row through the one static
+    # area: 8 kv heads, then a single-launch call with 128 kv heads (1 row,
+    # 128 q heads, dim 128, 2 splits), then 8 again.  The counter words of
+    # the wide call must not hold partial words of the first call, and its
+    # partials must not land on counter words the third call needs at zero.
+    cases = [(W.synth_case(1, 32, 8, 128, 64, 8192, seed=72), 2048),
+             (W.synth_case(1, 128, 128, 128, 64, 2048, seed=73), 1024),
+             (W.synth_case(1, 32, 8, 128, 64, 8192, seed=74), 2048)]
+    for i, (case, st) in enumerate(cases):
+        dc = DeviceCase(case)
+        name = kvb.selected_kernel_name(case.shape, dc.inp, st, fused=True)
+        log(f"no-alloc sequence call {i}: shape={case.shape.as_tuple()} split_tokens={st} kernel={name}")
+        assert ",true,false>" in name, f"call {i} is not a single launch: {name}"
+        a = _run(dc, st, noalloc=True)
+        b = _run(dc, st, noalloc=False)
+        for x, y, nm in zip(a, b, ("m", "l", "n", "out")):
+            assert np.array_equal(x.view(np.uint8), y.view(np.uint8)), f"call {i}: {nm} differs"
+        check_against_oracle(case, a[:3], f"no-alloc sequence call {i}", O.fp64(case, threads=8))
