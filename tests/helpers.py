@@ -82,3 +82,36 @@ def check_against_oracle(case, mln, label, ref=None, strict=False):
     if strict:
         assert g["strict_pass"], f"{label}: per-element gate 3e-6 + 5e-5|r| failed: {g}"
     return g
+
+
+def poison_unneeded(case, k_code=127, v_code=-128, scale=1.0e4):
+    """Copy of `case` with every cache slot the call must not read overwritten:
+    K code 127, V code -128 (fp32 KV: K 127 * scale, V -128 * scale) and large
+    finite k/v scales -- the future-poison idea of the reference's oracle test
+    (tests/reference_test.cpp:21-30) applied to the whole pool.  A slot is
+    needed only when it holds a logical token t of [begin, end) with
+    k_positions[t] <= max(q_positions); every other slot is poisoned: tokens
+    in the future of every query row, tokens before begin, slots past end in
+    a partial last page, and physical pages no logical page of the range maps
+    to.  Returns (poisoned case, number of poisoned (page, slot) pairs)."""
+    import copy
+
+    s = case.shape
+    P = s.page_tokens
+    need = np.zeros((s.pages, P), bool)
+    qmax = int(np.max(case.qpos)) if s.rows > 0 else -1
+    for t in range(s.begin, s.end):
+        if int(case.kpos[t]) <= qmax:
+            need[int(case.table[t // P]), t % P] = True
+    bad = ~need
+    c = copy.deepcopy(case)
+    if s.int8:
+        kk, vv = np.int8(k_code), np.int8(v_code)
+    else:
+        kk, vv = np.float32(k_code * scale), np.float32(v_code * scale)
+    pg, sl = np.nonzero(bad)
+    c.k[pg, :, sl, :] = kk
+    c.v[pg, :, :, sl] = vv
+    c.ks[pg, :, sl] = np.float32(scale)
+    c.vs[pg, :, sl] = np.float32(scale)
+    return c, int(bad.sum())
