@@ -79,8 +79,27 @@ template <class... T>
 __device__ __forceinline__ void lds_fence(T&... v) {
   (lds_fence1(v), ...);
 }
+// Wait for every vector-memory operation of this wave.
 template <uint32_t N>
-__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory"); }
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N == 0, "hand-counted waits go through wait_vm_keep");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+// Hand-counted wait: retire all but the N most recent vector-memory
+// operations, where N is what the KEEP most recent tile DMA groups of this
+// wave are meant to hold, so that every older group has landed.  N is a
+// count of emitted instructions, which the source cannot see: each group
+// starts with dma_group_mark(), and check_vm_waits.py verifies on the
+// device assembly, along every path, that such a wait leaves no operation of
+// an older group in flight (the KEEP value travels in an assembler comment).
+template <uint32_t N, uint32_t KEEP>
+__device__ __forceinline__ void wait_vm_keep() {
+  static_assert(N > 0 && N <= 63 && KEEP > 0, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) ; kvb-keep %1" ::"i"(N), "i"(KEEP) : "memory");
+}
+// Start of one tile's DMA group in the device assembly (an assembler
+// comment, no instruction).
+__device__ __forceinline__ void dma_group_mark() { asm volatile(";kvb-dma-group"); }
 
 struct Ctx {
   const int8_t* __restrict__ k;

@@ -284,6 +284,7 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
   auto issue_tile_of = [&](auto wtc, const auto& ppc, uint32_t k, uint8_t* buf, uint32_t prt)
                            __attribute__((always_inline)) {
     constexpr uint32_t W2 = decltype(wtc)::value;
+    dma_group_mark();
     if constexpr (PT) {
       const uint32_t lp = k * kTileTokens / a.page_tokens;
       const uint32_t rel = lp - c.lp_lo;
@@ -316,11 +317,11 @@ __global__ __launch_bounds__(64 * kWaves) void split_i8_rows_kernel(
     if (idle_dma || !issued(p + 1u)) {
       wait_vm<0>();
     } else if (WT == 1u) {
-      wait_vm<Part::kK + Part::kV + 2>();
+      wait_vm_keep<Part::kK + Part::kV + 2, 1>();
     } else if (part < 2u) {
-      wait_vm<Part::kK + Part::kV + 1>();
+      wait_vm_keep<Part::kK + Part::kV + 1, 1>();
     } else {
-      wait_vm<Part::kK + Part::kV>();
+      wait_vm_keep<Part::kK + Part::kV, 1>();
     }
   };
 
@@ -831,6 +832,7 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
   auto issue = [&](uint32_t t) __attribute__((always_inline)) {  // tile t of the range into slot t % 4
     uint8_t* const buf = smem + (t % kPcSlots) * kImg;
     const uint32_t k = k_first + t;
+    dma_group_mark();
     if constexpr (PT) {
       const uint32_t lp = k * kTileTokens / a.page_tokens;
       const uint32_t rel = lp - c.lp_lo;
@@ -867,20 +869,36 @@ __global__ __launch_bounds__(64 * kPcWaves) void split_i8_rows_pc_kernel(
     // Tile s landed: the wave's loads are tiles s and s + 1, each exactly
     // kLoadsPerTile vector-memory instructions when the page-table window
     // covers the range (no table load inside an issue); else wait for all.
+    // The emitted count per tile is checked on the device assembly
+    // (check_vm_waits.py: the wait leaves only the newest tile in flight).
     static_assert(G::kLoadsPerTile == 34u, "the tile's DMA instruction count");
     const bool window = ntiles > 0u && c.lp_hi - c.lp_lo < 64u;
+    // The page-table window comes from a vector load; consume it here, on
+    // every path (the first issue needs it anyway), so that no wait the
+    // compiler derives from it lands inside the step loop.
+    asm volatile("" : "+v"(c.ptab));
     // The QK waves' own loads (Q, positions) go out first, chip-wide ahead
     // of the tiles, so their round trip does not queue behind the DMA (a
     // bare s_barrier: no wait for those loads).
     bare_barrier();
     if (ntiles > 0u) issue(0u);
     if (ntiles > 1u) issue(1u);
+    // Tiles 0 and 1 both land before the first step, so tile 2 goes out
+    // only after them: issuing it as soon as tile 0 has landed measured
+    // slower (1,024-token splits at the dense geometry: 44.3 against 41.0 us
+    // per call), the chip-wide start then having a third tile per work-group
+    // in flight.
+    wait_vm<0>();
     for (uint32_t s = 0; s <= ntiles; ++s) {
       if (s < ntiles) {
-        if (s + 1u < ntiles && window) wait_vm<G::kLoadsPerTile>();
+        if (s + 1u < ntiles && window) wait_vm_keep<G::kLoadsPerTile, 1>();
         else wait_vm<0>();
       }
-      __syncthreads();  // tile s visible to all; every wave is done with step s - 1
+      // Tile s visible to all; every wave is done with step s - 1.  A bare
+      // s_barrier: this wave's only memory operations are the tile loads,
+      // which the wait above covers, and __syncthreads's release fence
+      // would add a wait for every load in flight (tile s + 1 too).
+      bare_barrier();
       if (s + 2u < ntiles) issue(s + 2u);
     }
     return;

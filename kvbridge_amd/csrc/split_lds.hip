@@ -251,7 +251,8 @@ __global__ __launch_bounds__(64 * NW) void split_lds_kernel(
     ip.lp = ip.k * kTileTokens / a.page_tokens;
     ip.slot = ip.k * kTileTokens - ip.lp * a.page_tokens;
   }
-  auto issue_next = [&](uint32_t seq, uint8_t* buf) {
+  auto issue_next = [&](uint32_t seq, uint8_t* buf) __attribute__((always_inline)) {
+    dma_group_mark();
     if constexpr (PT) {
       const uint32_t rel = ip.lp - c.lp_lo;
       uint32_t phys = rel < 64u ? __builtin_amdgcn_readlane(c.ptab, rel) : table[ip.lp];
@@ -363,7 +364,8 @@ __global__ __launch_bounds__(64 * NW) void split_lds_kernel(
     const uint32_t i = i0 + u;
     if (i < nt) {
       issue_next(i + NB - 1, ring + ((u + NB - 1) % NB) * G::kBufBytes);
-      wait_vm<kWait>();  // tile i has landed in slot u
+      if constexpr (NB > 1) wait_vm_keep<kWait, NB - 1>();  // tile i has landed in slot u
+      else wait_vm<0>();
       const uint32_t k = tile_of(i);
       compute_tile<D, u * G::kBufBytes>(st, ring_addr, ro, k, qh, ql, qlo, cq, is_full(k), s0, e_h,
                                         e_max, lane);
