@@ -129,14 +129,13 @@ int main(int argc, char** argv) {
               hipMalloc(&m, 8) == hipSuccess && hipMalloc(&l, 8) == hipSuccess && hipMalloc(&n, 2 * 64 * 4) == hipSuccess;
     expect(ok, "device allocations");
     if (!ok) return 1;
-    hipMemcpy(q, hq.data(), hq.size() * 4, hipMemcpyHostToDevice);
-    hipMemcpy(ks, hks.data(), 64, hipMemcpyHostToDevice);
-    hipMemcpy(vs, hvs.data(), 64, hipMemcpyHostToDevice);
-    hipMemcpy(qp, &qpos, 8, hipMemcpyHostToDevice);
-    hipMemcpy(kp, &kpos, 8, hipMemcpyHostToDevice);
-    hipMemcpy(tb, &table, 4, hipMemcpyHostToDevice);
-    hipMemcpy(k, hk.data(), hk.size(), hipMemcpyHostToDevice);
-    hipMemcpy(v, hv.data(), hv.size(), hipMemcpyHostToDevice);
+    const auto h2d = [](void* dst, const void* src, size_t bytes) {
+      return hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice) == hipSuccess;
+    };
+    expect(h2d(q, hq.data(), hq.size() * 4) && h2d(ks, hks.data(), 64) && h2d(vs, hvs.data(), 64) &&
+               h2d(qp, &qpos, 8) && h2d(kp, &kpos, 8) && h2d(tb, &table, 4) && h2d(k, hk.data(), hk.size()) &&
+               h2d(v, hv.data(), hv.size()),
+           "uploads");
     const kvbridge::DeviceInput in{q, qp, kp, tb, k, v, ks, vs};
     try {
       kvbridge::launch_attention(one, in, sc, m, l, n, nullptr);
@@ -146,9 +145,10 @@ int main(int argc, char** argv) {
     }
     expect(hipDeviceSynchronize() == hipSuccess, "device synchronize");
     float hm[2], hl[2], hn[128];
-    hipMemcpy(hm, m, 8, hipMemcpyDeviceToHost);
-    hipMemcpy(hl, l, 8, hipMemcpyDeviceToHost);
-    hipMemcpy(hn, n, sizeof(hn), hipMemcpyDeviceToHost);
+    expect(hipMemcpy(hm, m, 8, hipMemcpyDeviceToHost) == hipSuccess &&
+               hipMemcpy(hl, l, 8, hipMemcpyDeviceToHost) == hipSuccess &&
+               hipMemcpy(hn, n, sizeof(hn), hipMemcpyDeviceToHost) == hipSuccess,
+           "downloads");
     const float score = 0.125f * 64 * 0.5f * 3 * 0.25f;  // scale * sum_d q * k_code * k_scale
     for (int h = 0; h < 2; ++h) {
       expect(std::fabs(hm[h] - score) <= 1e-5f * score, "m is the single token's score");
