@@ -72,7 +72,11 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true", help="skip the gates (profiling runs only)")
     ap.add_argument("--no-graph", action="store_true", help="skip the hipGraph replays (profiling runs)")
+    ap.add_argument("--no-fenced", action="store_true",
+                    help="skip the fenced-ticket diagnostic single launch (kvb_decode_attention_fused_fenced)")
     ap.add_argument("--no-five-layer", action="store_true", help="skip the five-layer graph step (configs[4])")
+    ap.add_argument("--five-layer-only", action="store_true",
+                    help="run only the five-layer graph step and its eager comparison (kernel-trace runs)")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched configs[2] / configs[3] timings")
     ap.add_argument("--no-mma-geometry", action="store_true",
                     help="skip the rows-8 / group-6 / dim-256 / page-32 launch_attention_mma timing")
@@ -113,8 +117,13 @@ def main():
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
     def timed(fn, steps):
-        """ms per call of `steps` back-to-back calls fn(i), HIP events on the launch stream."""
+        """ms per call of `steps` back-to-back calls fn(i), HIP events on the
+        launch stream.  One untimed call fn(-1) is queued before the start
+        event, so the span opens when the device is already busy and holds
+        exactly `steps` calls of device time: the host's first submission
+        (up to tens of us for a graph launch) is not inside it."""
         torch.cuda.synchronize()
+        fn(-1)
         e0.record(stream)
         for i in range(steps):
             fn(i)
@@ -202,8 +211,11 @@ def main():
             host_case[c] = (case, O.fp64(case, threads=host_threads))
         return host_case[c]
 
-    def gate_out(label, out_f32, c=0):
-        """North-star gate of a normalized [rh, D] output against FP64 (copy c)."""
+    def gate_out(label, out_f32, c=0, bits0=None):
+        """North-star gate of a normalized [rh, D] output against FP64 (copy
+        c); bits0: the fp16 output's bytes instead of out_f32."""
+        if bits0 is not None:
+            out_f32 = bits0.view(np.float16).astype(np.float32)
         _, (ref, _) = fp64_ref(c)
         g = O.gates(out_f32.reshape(-1, D), ref)
         res = {"oracle": "fp64", "max_abs": g["max_abs"], "rel_l2": g["rel_l2"], "pass": bool(g["pass"]),
@@ -212,6 +224,72 @@ def main():
         if not g["pass"]:
             fail(f"parity failed: {label}", parity=res)
         return res
+
+    def five_layer_step():
+        """five independent cfg2 layers (copies 0..4),
+        each one fused decode call, captured as one hipGraph step and
+        replayed; every layer gated, replays bitwise equal to the eager step."""
+        five = {}
+        layers = list(range(min(5, copies)))
+        extra = []
+        while len(layers) + len(extra) < 5:
+            _, t_ = W.torch_cache(rows, qh, kvh, D, P, T, seed=0x4B56430 + len(extra), device="cuda:0")
+            extra.append(t_)
+        linps = [inps[i] for i in layers] + [kvb.device_input(t_["q"], t_["qpos"], t_["kpos"], t_["table"], t_["k"],
+                                                             t_["v"], t_["ks"], t_["vs"]) for t_ in extra]
+        lbufs = [dict(sc=torch.empty_like(scratch), cnt=torch.zeros(kvh, dtype=torch.int32, device=dev),
+                      m=torch.empty_like(m), l=torch.empty_like(l), n=torch.empty_like(n),
+                      o=torch.empty_like(out)) for _ in linps]
+
+        def five_step(strm):
+            for li, b in zip(linps, lbufs):
+                kvb.decode_attention_fused(s, li, st, b["sc"], b["cnt"], b["m"], b["l"], b["n"], b["o"],
+                                           kvb.KVB_OUT_F16, strm)
+
+        five_step(sp)
+        torch.cuda.synchronize()
+        eager_layers = [bits(b["o"]) for b in lbufs]
+        if gate:
+            five["parity"] = [gate_out(f"five-layer step, layer {k} (eager)", lbufs[k]["o"].float().cpu().numpy(),
+                                       c=layers[k])
+                              for k in range(len(layers))]
+        gs5 = torch.cuda.Stream()
+        gs5.wait_stream(stream)
+        with torch.cuda.stream(gs5):
+            five_step(gs5.cuda_stream)
+        torch.cuda.synchronize()
+        g5 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g5, stream=gs5):
+            five_step(gs5.cuda_stream)
+        step_ms = warm_and_time(lambda i: g5.replay(), steps=max(64, args.steps // 5), warmup=5)
+        replay_ok = all(np.array_equal(bits(b["o"]), e) for b, e in zip(lbufs, eager_layers))
+        if not replay_ok:
+            fail("five-layer graph replay differs from the eager step")
+        eager_step_ms = warm_and_time(lambda i: five_step(sp), steps=max(64, args.steps // 5), warmup=5)
+        # The same step captured twice into one graph: what one replay costs
+        # beyond its kernels (the step graph against two steps per replay).
+        g10 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g10, stream=gs5):
+            five_step(gs5.cuda_stream)
+            five_step(gs5.cuda_stream)
+        two_step_ms = warm_and_time(lambda i: g10.replay(), steps=max(32, args.steps // 10), warmup=3) / 2
+        if not all(np.array_equal(bits(b["o"]), e) for b, e in zip(lbufs, eager_layers)):
+            fail("two-step graph replay differs from the eager step")
+        step_us = step_ms * 1e3
+        five.update({"layers": 5, "us_per_step": round(step_us, 3), "GB/s": round(gbs(5 * kv_bytes, step_us), 1),
+                     "pct_of_peak": round(100.0 * gbs(5 * kv_bytes, step_us) / HBM_PEAK_GBS, 2),
+                     "kv_bytes_per_step": 5 * kv_bytes, "graph": True, "replay_bitwise_equal_to_eager": replay_ok,
+                     "eager_us_per_step": round(eager_step_ms * 1e3, 3),
+                     "two_steps_per_replay_us_per_step": round(two_step_ms * 1e3, 3),
+                     "replay_overhead_us": round(2e3 * (step_ms - two_step_ms), 3)})
+        log(f"five-layer graph step: {step_us:.2f} us ({five['GB/s']:.0f} GB/s); eager {eager_step_ms*1e3:.2f} us; "
+            f"two steps per replay {two_step_ms*1e3:.2f} us per step")
+        del extra, lbufs, g5, g10
+        return five
+
+    if args.five_layer_only:  # profiling runs: this leg alone, one JSON line
+        print(json.dumps({"metric": METRIC, "five_layer_step": five_layer_step()}), flush=True)
+        return
 
     # ---- gate of the benchmarked call, then the headline timing
     parity = None
@@ -243,6 +321,25 @@ def main():
     p50, p95 = statistics.median(per_iter), per_iter[int(math.ceil(0.95 * len(per_iter))) - 1]
     log(f"fused call: {eager_ms*1e3:.2f} us/call back to back ({args.steps} calls after {settle_calls} settle + "
         f"{args.warmup} warmup); per-iteration events p50 {p50:.2f} p95 {p95:.2f} us; repeat bitwise {repeat_ok}")
+
+    # ---- diagnostic: the same single launch with formal release / acquire
+    # fences around the merge ticket (kvb_decode_attention_fused_fenced), the
+    # ordering the benchmarked call replaces with agent-scope atomic partials.
+    fenced = None
+    if not args.no_fenced:
+        def call_fenced(i):
+            kvb.decode_attention_fused_fenced(s, inps[i % copies], st, scratch, counters, m, l, n, out,
+                                              kvb.KVB_OUT_F16, sp)
+
+        fenced = {"kernel": "split_i8_kernel<128,8,2,true,4,true,false,true>"}
+        before_f = outputs_of(call_fenced)
+        fenced["bitwise_equal_to_fused"] = same(before, before_f)
+        if not fenced["bitwise_equal_to_fused"]:
+            fail("fenced single launch differs from the benchmarked call")
+        if gate:
+            fenced["parity"] = gate_out("fenced single launch (copy 0)", None, c=0, bits0=before_f[0])
+        fenced["us_per_call"] = round(warm_and_time(call_fenced) * 1e3, 3)
+        log(f"fenced single launch (diagnostic): {fenced['us_per_call']:.2f} us/call")
 
     # ---- two launches: split kernel + merge kernel
     two = {}
@@ -293,7 +390,7 @@ def main():
                 kvb.decode_attention_fused(s, inps[c], st, scratch, counters, m, l, n, out, kvb.KVB_OUT_F16,
                                            gs.cuda_stream)
         torch.cuda.synchronize()
-        reps = max(3, -(-args.steps // copies))
+        reps = max(64, -(-args.steps // copies))  # at least 64 replays, whatever --steps
         gms = warm_and_time(lambda i: g.replay(), steps=reps, warmup=3) / copies
         graph_ok = np.array_equal(bits(out), before[copies - 1])
         if not graph_ok:
@@ -398,54 +495,10 @@ def main():
                 f"({gbs(abytes, aus):.0f} GB/s); eager loop {eager_us:.2f} us")
         del ak, av, aks, avs
 
-    # ---- five independent cfg2 layers (copies 0..4),
-    # each one fused decode call, captured as one hipGraph step and replayed.
+    # ---- five independent cfg2 layers in one hipGraph step
     five = None
     if not args.no_five_layer and not args.no_graph:
-        layers = list(range(min(5, copies)))
-        extra = []
-        while len(layers) + len(extra) < 5:
-            _, t_ = W.torch_cache(rows, qh, kvh, D, P, T, seed=0x4B56430 + len(extra), device="cuda:0")
-            extra.append(t_)
-        linps = [inps[i] for i in layers] + [kvb.device_input(t_["q"], t_["qpos"], t_["kpos"], t_["table"], t_["k"],
-                                                             t_["v"], t_["ks"], t_["vs"]) for t_ in extra]
-        lbufs = [dict(sc=torch.empty_like(scratch), cnt=torch.zeros(kvh, dtype=torch.int32, device=dev),
-                      m=torch.empty_like(m), l=torch.empty_like(l), n=torch.empty_like(n),
-                      o=torch.empty_like(out)) for _ in linps]
-
-        def five_step(strm):
-            for li, b in zip(linps, lbufs):
-                kvb.decode_attention_fused(s, li, st, b["sc"], b["cnt"], b["m"], b["l"], b["n"], b["o"],
-                                           kvb.KVB_OUT_F16, strm)
-
-        five_step(sp)
-        torch.cuda.synchronize()
-        eager_layers = [bits(b["o"]) for b in lbufs]
-        five = {}
-        if gate:
-            five["parity"] = [gate_out(f"five-layer step, layer {k} (eager)", lbufs[k]["o"].float().cpu().numpy(),
-                                       c=layers[k])
-                              for k in range(len(layers))]
-        gs5 = torch.cuda.Stream()
-        gs5.wait_stream(stream)
-        with torch.cuda.stream(gs5):
-            five_step(gs5.cuda_stream)
-        torch.cuda.synchronize()
-        g5 = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g5, stream=gs5):
-            five_step(gs5.cuda_stream)
-        step_ms = warm_and_time(lambda i: g5.replay(), steps=max(10, args.steps // 5), warmup=5)
-        replay_ok = all(np.array_equal(bits(b["o"]), e) for b, e in zip(lbufs, eager_layers))
-        if not replay_ok:
-            fail("five-layer graph replay differs from the eager step")
-        eager_step_ms = warm_and_time(lambda i: five_step(sp), steps=max(10, args.steps // 5), warmup=5)
-        step_us = step_ms * 1e3
-        five.update({"layers": 5, "us_per_step": round(step_us, 3), "GB/s": round(gbs(5 * kv_bytes, step_us), 1),
-                     "pct_of_peak": round(100.0 * gbs(5 * kv_bytes, step_us) / HBM_PEAK_GBS, 2),
-                     "kv_bytes_per_step": 5 * kv_bytes, "graph": True, "replay_bitwise_equal_to_eager": replay_ok,
-                     "eager_us_per_step": round(eager_step_ms * 1e3, 3)})
-        log(f"five-layer graph step: {step_us:.2f} us ({five['GB/s']:.0f} GB/s); eager {eager_step_ms*1e3:.2f} us")
-        del extra, lbufs, g5
+        five = five_layer_step()
 
     # ---- BASELINE configs[2] (16 ragged sequences) and configs[3] (4 x 131072
     # tokens, GQA 8): the batched call, with counters given (one launch where
@@ -696,7 +749,8 @@ def main():
                    "splits": splits},
         "timing": {"settle_seconds": args.settle_seconds, "settle_calls": settle_calls,
                    "graph_packet_capture_env": os.environ.get("DEBUG_CLR_GRAPH_PACKET_CAPTURE"),
-                   "method": "back-to-back calls, HIP events on the launch stream",
+                   "method": "back-to-back calls, HIP events on the launch stream; one untimed call queued "
+                             "before the start event of every timed section (graph legs: >= 64 replays)",
                    "per_call_events_us": {"p50": round(p50, 3), "p95": round(p95, 3), "min": round(per_iter[0], 3),
                                           "warmup": 8, "iters": 32},
                    "repeat_bitwise": repeat_ok},
@@ -705,6 +759,7 @@ def main():
                      "kernel": fused_kernel, "algorithmic_bytes_per_launch": kv_bytes,
                      "launch_us": round(call_ms * 1e3, 3)},
         "two_launch": two,
+        "fused_fenced": fenced,
         "launch_attention_256_token_splits": ref_api,
         "graph": graph,
         "split_only": {"kernel": split_kernel, "us": round(split_ms * 1e3, 3),

@@ -224,11 +224,22 @@ int kvb_decode_attention_noalloc(const kvb_shape* s, const kvb_device_input* in,
 int kvb_selected_kernel(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens);
 /* Extension (diagnostic): name of the kernel instance kvb_split_attention
  * (fused = 0) or kvb_decode_attention_fused (fused != 0) would launch, as
- * rocprofv3 reports it, e.g. "split_i8_kernel<128,8,2,true,4,false>"; "" if
+ * rocprofv3 reports it, e.g. "split_i8_kernel<128,8,2,true,4,false,false,false>"; "" if
  * the arguments are invalid.  Points to thread-local or static storage. */
 const char* kvb_selected_kernel_name(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens,
                                      int fused);
 
+/* Extension (diagnostic): kvb_decode_attention_fused with formal agent-scope
+ * release / acquire fences around the merge ticket (a memory-model-formal
+ * ordering of the partials; the default call gets the same ordering from
+ * agent-scope atomic partial stores and loads, without the L2 write-back and
+ * invalidate these fences add).  Same arguments and results, bitwise; only
+ * the eight-wave dim-128 single launch (<= 4 head-rows per kv head, pages of
+ * >= 64 tokens, splits of >= 16 tiles) has an instance, other calls return
+ * KVB_EINVAL.  For measuring that ordering choice, not for production use. */
+int kvb_decode_attention_fused_fenced(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens,
+                                      float* scratch, uint32_t* counters, float* m, float* l, float* n, void* out,
+                                      int out_type, void* stream);
 /* Extension (diagnostic, no counterpart in the reference library): streams
  * `bytes` (a multiple of 16) of device memory with non-temporal 16-byte loads
  * over `blocks` work-groups of 512 threads (contiguous runs of 8 KiB items per

@@ -164,6 +164,16 @@ def decode_attention_fused(s: Shape, inp: DeviceInput, split_tokens: int, scratc
                                             _stream(stream)))
 
 
+def decode_attention_fused_fenced(s: Shape, inp: DeviceInput, split_tokens: int, scratch, counters, m, l, n,
+                                  out=None, out_type: int = KVB_OUT_NONE, stream=None) -> None:
+    """Diagnostic (kvb_decode_attention_fused_fenced): the single launch with
+    formal release / acquire fences around the merge ticket; bitwise the
+    same results as decode_attention_fused."""
+    check(load().kvb_decode_attention_fused_fenced(ctypes.byref(s), ctypes.byref(inp), split_tokens, _ptr(scratch),
+                                                   _ptr(counters), _ptr(m), _ptr(l), _ptr(n), _ptr(out), out_type,
+                                                   _stream(stream)))
+
+
 def decode_attention_noalloc(s: Shape, inp: DeviceInput, split_tokens: int, m, l, n, out=None,
                              out_type: int = KVB_OUT_NONE, stream=None) -> None:
     """Single-launch decode with the library's fixed 8 MiB per-device scratch

@@ -139,6 +139,7 @@ SIGNATURES = [
     ("kvb_merge_finalize", _INT, [_SP, _VP, _U32, _VP, _VP, _VP, _VP, _INT, _VP]),
     ("kvb_decode_attention", _INT, [_SP, _IP, _U32, _VP, _VP, _VP, _VP, _VP, _INT, _VP]),
     ("kvb_decode_attention_fused", _INT, [_SP, _IP, _U32, _VP, _VP, _VP, _VP, _VP, _VP, _INT, _VP]),
+    ("kvb_decode_attention_fused_fenced", _INT, [_SP, _IP, _U32, _VP, _VP, _VP, _VP, _VP, _VP, _INT, _VP]),
     ("kvb_decode_attention_noalloc", _INT, [_SP, _IP, _U32, _VP, _VP, _VP, _VP, _INT, _VP]),
     ("kvb_selected_kernel", _INT, [_SP, _IP, _U32]),
     ("kvb_selected_kernel_name", ctypes.c_char_p, [_SP, _IP, _U32, _INT]),

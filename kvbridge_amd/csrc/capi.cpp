@@ -446,6 +446,35 @@ int kvb_decode_attention_fused(const kvb_shape* sp, const kvb_device_input* ip, 
   });
 }
 
+int kvb_decode_attention_fused_fenced(const kvb_shape* sp, const kvb_device_input* ip, uint32_t split_tokens,
+                                      float* scratch, uint32_t* counters, float* m, float* l, float* n, void* out,
+                                      int out_type, void* stream) {
+  return guarded([&]() -> int {
+    if (!sp || !ip) return fail(KVB_EINVAL, "shape and input descriptors must be non-null");
+    const kvbridge::Shape s = to_shape(*sp);
+    const kvbridge::DeviceInput in = to_input(*ip);
+    if (const char* e = outputs_error(s, scratch, m, l, n)) return fail(KVB_EINVAL, e);
+    if (const char* e = launch_error(s, in, scratch)) return fail(KVB_EINVAL, e);
+    if (!counters) return fail(KVB_EINVAL, "counters must be a non-null device buffer");
+    if (out_type != KVB_OUT_NONE && out_type != KVB_OUT_F32 && out_type != KVB_OUT_F16)
+      return fail(KVB_EINVAL, "unknown output type");
+    if (out_type != KVB_OUT_NONE && !out) return fail(KVB_EINVAL, "output buffer must be non-null");
+    const unsigned splits = kvbridge::split_count(s, split_tokens);
+    kvb::SplitArgs a = kvb::make_split_args(s, in, split_tokens, splits, scratch);
+    a.counters = counters;
+    a.m = m;
+    a.l = l;
+    a.n = n;
+    a.out = out;
+    a.out_type = out_type;
+    if (!kvb::tiled_supported(s, in) || !kvb::i8_fenced_supported(a))
+      return fail(KVB_EINVAL,
+                  "the fenced diagnostic call covers only the eight-wave dim-128 single launch "
+                  "(<= 4 head-rows per kv head, pages of >= 64 tokens, splits of >= 16 tiles)");
+    return hip_status(kvb::launch_split_i8_fenced(a, static_cast<hipStream_t>(stream)), "fenced decode launch");
+  });
+}
+
 int kvb_hbm_read_probe(const void* src, size_t bytes, uint32_t* sink, uint32_t blocks, void* stream) {
   if (!src || !sink || bytes % 16 != 0 || blocks == 0)
     return fail(KVB_EINVAL, "probe needs non-null 16-byte-multiple source, a sink and blocks > 0");

@@ -61,6 +61,10 @@ hipError_t launch_split_lds(const SplitArgs& a, hipStream_t stream);  // LDS-DMA
 hipError_t launch_split_i8(const SplitArgs& a, hipStream_t stream);   // register-staged tiles, int8 MFMA
 bool i8_supported(const SplitArgs& a);  // head_rows <= 8 (<= 4 at dim 256), power-of-two pages
 bool i8_fusable(const SplitArgs& a);    // the int8 kernel can run the fused merge
+// Diagnostic: the fused launch with formal release / acquire fences around
+// the merge ticket (eight-wave dim-128 page-tile configuration only).
+bool i8_fenced_supported(const SplitArgs& a);
+hipError_t launch_split_i8_fenced(const SplitArgs& a, hipStream_t stream);
 // Int8-MFMA kernel for more than 8 head-rows over short tile-aligned splits
 // (one work-group per split and kv head, the split's tiles held in LDS).
 hipError_t launch_split_i8_rows(const SplitArgs& a, hipStream_t stream);

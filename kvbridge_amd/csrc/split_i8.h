@@ -378,7 +378,13 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
 // kernel-argument preloading for them (the dispatcher places them in SGPRs),
 // so the page-table load is issued without waiting for a kernel-argument
 // load.  They duplicate fields of a_in, which the kernel overrides with them.
-template <int D, int NW, int NB, bool PT, int HS, bool FUSED, bool VARLEN>
+//
+// FENCE (one diagnostic instance, kvb_decode_attention_fused_fenced): the
+// single launch with the formal agent-scope release fence before every
+// ticket and an acquire fence after the merger's -- the ordering the other
+// instances get from agent-scope atomic partials, without the L2 write-back
+// and invalidate these fences add.
+template <int D, int NW, int NB, bool PT, int HS, bool FUSED, bool VARLEN, bool FENCE>
 __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
     const uint32_t* __restrict__ table_in, const int8_t* __restrict__ kdata, const float* __restrict__ kscale,
     const float* __restrict__ vscale, uint32_t p_begin, uint32_t p_end, uint32_t p_split_tokens,
@@ -937,6 +943,7 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
     // completed, the work-group synchronizes, and only then takes a ticket,
     // so the work-group that draws the last ticket sees every partial.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if constexpr (FENCE) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
     if (threadIdx.x == 0) {
       const uint32_t t = __hip_atomic_fetch_add(a.counters + kv, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -944,6 +951,7 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
     }
     __syncthreads();
     if (last_s != 0u) {
+      if constexpr (FENCE) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       static_assert(MergeRowsLayout<D, NW, (uint32_t(HS) * D / 4u <= 64u * NW ? HS : 1)>::kFloats * 4u <= L::kBytes,
                     "the merge's LDS fits the kernel's");
       float* f_s = reinterpret_cast<float*>(smem);  // [HS][32] split factors or the merge_rows area
@@ -965,28 +973,28 @@ hipError_t launch_cfg(const SplitArgs& a, hipStream_t stream) {
   const dim3 block(64 * NW);
   if (varlen && !pt) return hipErrorInvalidValue;  // batched calls need whole-tile pages (i8_supported)
   if (varlen && fused)
-    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, true, HS, true, true>), grid, block, 0, stream, KVB_I8_ARGS);
+    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, true, HS, true, true, false>), grid, block, 0, stream, KVB_I8_ARGS);
   else if (varlen)
-    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, true, HS, false, true>), grid, block, 0, stream, KVB_I8_ARGS);
+    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, true, HS, false, true, false>), grid, block, 0, stream, KVB_I8_ARGS);
   else if (pt && fused)
-    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, true, HS, true, false>), grid, block, 0, stream, KVB_I8_ARGS);
+    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, true, HS, true, false, false>), grid, block, 0, stream, KVB_I8_ARGS);
   else if (pt)
-    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, true, HS, false, false>), grid, block, 0, stream, KVB_I8_ARGS);
+    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, true, HS, false, false, false>), grid, block, 0, stream, KVB_I8_ARGS);
   else if (fused)
-    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, false, HS, true, false>), grid, block, 0, stream, KVB_I8_ARGS);
+    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, false, HS, true, false, false>), grid, block, 0, stream, KVB_I8_ARGS);
   else
-    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, false, HS, false, false>), grid, block, 0, stream, KVB_I8_ARGS);
+    hipLaunchKernelGGL((split_i8_kernel<D, NW, NB, false, HS, false, false, false>), grid, block, 0, stream, KVB_I8_ARGS);
   return hipGetLastError();
 }
 
 template <int D, int NW, int NB, int HS>
 hipError_t preload_cfg() {
-  const void* fns[] = {reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS, false, false>),
-                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, false, HS, false, false>),
-                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS, true, false>),
-                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, false, HS, true, false>),
-                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS, false, true>),
-                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS, true, true>)};
+  const void* fns[] = {reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS, false, false, false>),
+                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, false, HS, false, false, false>),
+                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS, true, false, false>),
+                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, false, HS, true, false, false>),
+                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS, false, true, false>),
+                       reinterpret_cast<const void*>(&split_i8_kernel<D, NW, NB, true, HS, true, true, false>)};
   hipFuncAttributes attr{};
   for (const void* f : fns) {
     const hipError_t e = hipFuncGetAttributes(&attr, f);

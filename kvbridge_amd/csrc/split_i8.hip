@@ -94,6 +94,19 @@ bool i8_fusable(const SplitArgs& a) {
   return (a.splits + per_pass - 1u) / per_pass <= 2u;
 }
 
+hipError_t launch_i8_fenced_d128(const SplitArgs& a, hipStream_t stream);
+
+// Diagnostic single launch with formal release / acquire fences: only the
+// eight-wave dim-128 page-tile configuration (cfg2's) has an instance.
+bool i8_fenced_supported(const SplitArgs& a) {
+  return a.dim == 128 && a.seq_starts == nullptr && a.page_tokens >= kTiles && i8_supported(a) && i8_fusable(a) &&
+         i8_config(a) == 82;
+}
+
+hipError_t launch_split_i8_fenced(const SplitArgs& a, hipStream_t stream) {
+  return i8_fenced_supported(a) ? launch_i8_fenced_d128(a, stream) : hipErrorInvalidValue;
+}
+
 hipError_t launch_split_i8(const SplitArgs& a, hipStream_t stream) {
   const int cfg = i8_config(a);
   switch (a.dim) {
@@ -107,7 +120,7 @@ hipError_t launch_split_i8(const SplitArgs& a, hipStream_t stream) {
 const char* i8_kernel_name(const SplitArgs& a) {
   static thread_local char buf[112];
   const int cfg = i8_config(a);
-  std::snprintf(buf, sizeof(buf), "split_i8_kernel<%u,%d,%d,%s,%d,%s,%s>", a.dim, cfg / 10, cfg % 10,
+  std::snprintf(buf, sizeof(buf), "split_i8_kernel<%u,%d,%d,%s,%d,%s,%s,false>", a.dim, cfg / 10, cfg % 10,
                 a.page_tokens >= kTiles ? "true" : "false", a.rows * a.group <= 4 ? 4 : 8,
                 a.counters != nullptr ? "true" : "false", a.seq_starts != nullptr ? "true" : "false");
   return buf;

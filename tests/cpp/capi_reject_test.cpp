@@ -166,6 +166,8 @@ static void launches_rejected() {
     expect_einval(kvb_decode_attention_fused(sp, &fake, 128, f, u, f, f, f, f, KVB_OUT_F32, nullptr),
                   "fused bad shape");
     expect_einval(kvb_decode_attention_noalloc(sp, &fake, 128, f, f, f, f, KVB_OUT_F32, nullptr), "noalloc bad shape");
+    expect_einval(kvb_decode_attention_fused_fenced(sp, &fake, 128, f, u, f, f, f, f, KVB_OUT_F32, nullptr),
+                  "fenced bad shape");
     expect_einval(kvb_paged_read_probe(sp, &fake, 128, u, nullptr), "paged probe bad shape");
     expect(kvb_selected_kernel(sp, &fake, 128) == 0, "selected_kernel of an invalid shape");
   }
@@ -187,6 +189,10 @@ static void launches_rejected() {
                 "fused null counters");
   expect_einval(kvb_decode_attention_fused(&s, &misaligned, 128, f, u, f, f, f, f, KVB_OUT_F32, nullptr),
                 "fused misaligned K");
+  // The fenced diagnostic call has an instance only for the eight-wave dim-128 launch.
+  expect_einval(kvb_decode_attention_fused_fenced(&s, &fake, 128, f, u, f, f, f, f, KVB_OUT_F32, nullptr),
+                "fenced unsupported shape");
+  expect(std::strstr(kvb_last_error(), "fenced diagnostic") != nullptr, "fenced shape message");
   // The static area of the no-alloc call cannot hold 64 q heads x 4,096 splits.
   const kvb_shape big = {1, 64, 8, 128, 64, 16384, 1u << 20, 0, 1u << 20, 0.0883883f, 1};
   expect_einval(kvb_decode_attention_noalloc(&big, &fake, 256, f, f, f, f, KVB_OUT_F16, nullptr), "noalloc too big");

@@ -75,23 +75,23 @@ def test_kernel_choice_names():
     inp = kvb.batch_input(fake, fake, fake, fake, fake, fake, fake, fake, fake, fake)
     # 4 x 64 splits x 8 kv heads = 2048 work-groups of 32-tile splits -> one wave per
     # work-group, no single launch (more than two work-groups per CU): split + merge kernels
-    assert kvb.batch_kernel_name(s, inp, fused=True) == "split_i8_kernel<128,1,2,true,8,false,true>"
-    assert kvb.batch_kernel_name(s, inp) == "split_i8_kernel<128,1,2,true,8,false,true>"
+    assert kvb.batch_kernel_name(s, inp, fused=True) == "split_i8_kernel<128,1,2,true,8,false,true,false>"
+    assert kvb.batch_kernel_name(s, inp) == "split_i8_kernel<128,1,2,true,8,false,true,false>"
     # one sequence: 512 work-groups -> four-wave groups
-    assert kvb.batch_kernel_name(s.copy(batch=1), inp) == "split_i8_kernel<128,4,2,true,8,false,true>"
+    assert kvb.batch_kernel_name(s.copy(batch=1), inp) == "split_i8_kernel<128,4,2,true,8,false,true,false>"
     # 4 head-rows, 2048 work-groups of 32-tile splits -> one wave, two launches;
     # 512 work-groups -> eight-wave single launch; 256 -> eight waves
     g4 = s.copy(q_heads=32)
-    assert kvb.batch_kernel_name(g4, inp) == "split_i8_kernel<128,1,2,true,4,false,true>"
-    assert kvb.batch_kernel_name(g4, inp, fused=True) == "split_i8_kernel<128,1,2,true,4,false,true>"
+    assert kvb.batch_kernel_name(g4, inp) == "split_i8_kernel<128,1,2,true,4,false,true,false>"
+    assert kvb.batch_kernel_name(g4, inp, fused=True) == "split_i8_kernel<128,1,2,true,4,false,true,false>"
     assert kvb.batch_kernel_name(g4.copy(batch=16, max_tokens=32768), inp, fused=True) == \
-        "split_i8_kernel<128,1,2,true,4,false,true>"
+        "split_i8_kernel<128,1,2,true,4,false,true,false>"
     # 2048 work-groups of 80-tile splits -> four waves
     assert kvb.batch_kernel_name(g4.copy(batch=16, max_tokens=81920, split_tokens=5120), inp) == \
-        "split_i8_kernel<128,4,2,true,4,false,true>"
+        "split_i8_kernel<128,4,2,true,4,false,true,false>"
     assert kvb.batch_kernel_name(g4.copy(max_tokens=32768), inp, fused=True) == \
-        "split_i8_kernel<128,8,2,true,4,true,true>"
-    assert kvb.batch_kernel_name(g4.copy(batch=1, max_tokens=65536), inp) == "split_i8_kernel<128,8,2,true,4,false,true>"
+        "split_i8_kernel<128,8,2,true,4,true,true,false>"
+    assert kvb.batch_kernel_name(g4.copy(batch=1, max_tokens=65536), inp) == "split_i8_kernel<128,8,2,true,4,false,true,false>"
     small_pages = s.copy(page_tokens=16, pages=8192 * 4, table_entries=8192 * 4)
     assert kvb.batch_kernel_name(small_pages, inp).startswith("split_generic_kernel<true, true>")
     assert kvb.batch_kernel_name(s.copy(batch=0), inp) == ""

@@ -123,3 +123,37 @@ def test_fused_rejects_null_counters(gpu):
     dc = DeviceCase(case)
     with pytest.raises(kvb.KvbInvalidArgument, match="counters"):
         kvb.decode_attention_fused(case.shape, dc.inp, st, dc.scratch(st), None, dc.m, dc.l, dc.n)
+
+
+def test_fenced_diagnostic_matches_fused(gpu):
+    # kvb_decode_attention_fused_fenced: the same single launch with formal
+    # release / acquire fences around the merge ticket.  Only the ordering
+    # instructions differ, so m, l, n and the fp16 output are bitwise those of
+    # the default call; shapes without an instance are rejected.
+    import torch
+
+    case = W.synth_case(1, 32, 8, 128, 64, 16384, seed=91, qpos=[12000])
+    dc = DeviceCase(case)
+    st = 1024  # 16 splits of 16 tiles: the eight-wave configuration
+    assert kvb.selected_kernel_name(case.shape, dc.inp, st, True) == "split_i8_kernel<128,8,2,true,4,true,false,false>"
+    s = case.shape
+    rh = s.rows * s.q_heads
+    res = []
+    for fn in (kvb.decode_attention_fused, kvb.decode_attention_fused_fenced):
+        counters = torch.zeros(s.kv_heads, dtype=torch.int32, device=dc.device)
+        out = torch.full((rh * s.dim,), float("nan"), dtype=torch.float16, device=dc.device)
+        for t in (dc.m, dc.l, dc.n):
+            t.fill_(float("nan"))
+        fn(s, dc.inp, st, dc.scratch(st), counters, dc.m, dc.l, dc.n, out, kvb.KVB_OUT_F16)
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(counters).item() == 0
+        res.append(dc.read() + (out.view(torch.int16).cpu().numpy().copy(),))
+    for x, y, nm in zip(res[0], res[1], ("m", "l", "n", "out")):
+        assert np.array_equal(x.view(np.uint8), y.view(np.uint8)), f"fenced call: {nm} differs"
+    check_against_oracle(case, res[1][:3], "fenced single launch", strict=True)
+    with pytest.raises(kvb.KvbInvalidArgument, match="fenced diagnostic"):
+        small = W.synth_case(1, 8, 2, 64, 16, 512, seed=92)
+        dcs = DeviceCase(small)
+        kvb.decode_attention_fused_fenced(small.shape, dcs.inp, 128, dcs.scratch(128),
+                                          torch.zeros(2, dtype=torch.int32, device=dcs.device),
+                                          dcs.m, dcs.l, dcs.n, None, kvb.KVB_OUT_NONE)
