@@ -4,6 +4,11 @@
 // fp32 scale and stored into its physical slot of the page pool:
 //   scale = absmax / 127 (1 when absmax == 0, all codes 0),
 //   code  = clamp(rint(x / scale), -127, 127)      (round half to even),
+// with fp32 IEEE semantics throughout, max and clamp as fmaxf / fminf:
+// non-finite sources give defined codes in every kernel -- NaN elements are
+// left out of the absmax, an infinite element makes the scale infinite
+// (finite elements then quantize to 0), and a NaN quotient (a NaN element,
+// or infinity over an infinite scale) clamps to -127;
 //   K codes token-major  k[((page*kv_heads + kv)*P + slot)*D + d],
 //   V codes dim-major    v[((page*kv_heads + kv)*D + d)*P + slot],
 //   scales               k_scales / v_scales[(page*kv_heads + kv)*P + slot].
@@ -65,34 +70,14 @@ __device__ __forceinline__ int8_t quantize(float x, float scale) {
   return int8_t(int(c));
 }
 
-// The codes of N elements of one row (|x| <= absmax, scale = absmax / 127):
-// quantize() for a row slice with the rounding done by one add.  t = x / s
-// + 1.5 * 2^23 lies in [2^23, 2^24), where the fp32 ulp is 1, so the add
-// rounds to the nearest integer (ties to even: rint) and t's low byte is the
-// code; |x / s| <= 127.00001, so no clamp is needed.  A lane with any element
-// near a half-integer recomputes its slice with the division.
 constexpr float kRoundMagic = 12582912.f;  // 1.5 * 2^23
-template <uint32_t N>
-__device__ __forceinline__ void quantize_slice(const float (&x)[N], float scale, uint32_t (&t)[N]) {
-  const float r = __builtin_amdgcn_rcpf(scale);
-  uint32_t amb = 0u;
-#pragma unroll
-  for (uint32_t e = 0; e < N; ++e) {
-    const float q = x[e] * r;
-    const float ti = q + kRoundMagic;
-    amb |= fabsf(q - (ti - kRoundMagic)) <= 0.5f - 0x1p-14f ? 0u : 1u;  // NaN counts as near
-    t[e] = __float_as_uint(ti);
-  }
-  if (amb != 0u) {  // rare: one branch per slice
-#pragma unroll
-    for (uint32_t e = 0; e < N; ++e) t[e] = __float_as_uint(x[e] / scale + kRoundMagic);
-  }
-}
 
 // |x| max of the N elements of type T in a 16-byte word (exact: max picks
-// an element).  fp16: the sign bits cleared, finite halves order like their
+// an element), NaN elements ignored like fmaxf does (as in the row and tile
+// kernels).  fp16: the sign bits cleared, non-NaN halves order like their
 // 16-bit patterns, so a packed unsigned 16-bit max (two elements an
-// instruction) finds the largest magnitude.
+// instruction) finds the largest magnitude; a NaN (pattern above infinity's
+// 0x7c00) wins that max, and such a word (rare) is redone element by element.
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 template <class T, uint32_t N>
 __device__ __forceinline__ float word_absmax(const u32x4& w) {
@@ -101,7 +86,12 @@ __device__ __forceinline__ float word_absmax(const u32x4& w) {
 #pragma unroll
     for (int j = 1; j < 4; ++j) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[j] & 0x7fff7fffu));
     const uint16_t b = m[0] > m[1] ? m[0] : m[1];
-    return float(__builtin_bit_cast(_Float16, b));
+    if (b <= 0x7c00u) return float(__builtin_bit_cast(_Float16, b));
+    const _Float16* e = reinterpret_cast<const _Float16*>(&w);
+    float a = 0.f;
+#pragma unroll
+    for (uint32_t i = 0; i < N; ++i) a = fmaxf(a, fabsf(float(e[i])));
+    return a;
   } else {
     const T* e = reinterpret_cast<const T*>(&w);
     float a = 0.f;
@@ -130,9 +120,10 @@ __device__ __forceinline__ void quantize_word(const u32x4& w, float scale, uint3
     amb |= fabsf(d) <= 0.5f - 0x1p-14f ? 0u : 1u;  // NaN counts as near
     t[i] = __float_as_uint(ti);
   }
-  if (amb != 0u) {  // rare: one branch per word
+  if (amb != 0u) {  // rare: one branch per word; the clamp of quantize() (a NaN quotient gives -127)
 #pragma unroll
-    for (uint32_t i = 0; i < N; ++i) t[i] = __float_as_uint(to_f32(e[i]) / scale + kRoundMagic);
+    for (uint32_t i = 0; i < N; ++i)
+      t[i] = __float_as_uint(fminf(fmaxf(__builtin_rintf(to_f32(e[i]) / scale), -127.f), 127.f) + kRoundMagic);
   }
 }
 

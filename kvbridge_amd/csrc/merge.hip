@@ -65,7 +65,8 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(
 // memory round trip (more splits take their maxima in a strided pass
 // first).  M = max_j m_j, f_j = e^(m_j - M) (0 where l_j = 0) shared through
 // LDS, L = sum_j f_j l_j, the group sums added in group order; slice 0
-// writes m and l.  Deterministic for a given S, D and DS.
+// writes m and l.  Deterministic for a given S, D and DS (DS is chosen from
+// the shape alone).
 constexpr uint32_t kSliceThreads = 256;
 
 template <int D, int DS>
@@ -179,12 +180,17 @@ __global__ __launch_bounds__(kSliceThreads) void merge_slices_kernel(
   }
 }
 
-// Slice width: the widest of 64 / 32 / 16 dims that still gives two
-// work-groups per compute unit, else 16.
+// Slice width: the widest of 64 / 32 / 16 dims that still gives 512
+// work-groups (two per compute unit of a whole MI355X), else 16.  The width
+// sets the split groups the sums are added in, so it is chosen from the
+// shape alone, not from the device's compute-unit count: the same call gives
+// the same bits on a partitioned device.
+constexpr uint64_t kSliceGroupsWanted = 512;
+
 template <int D>
 hipError_t launch_merge_slices(uint32_t row_heads, uint32_t splits, const float* scratch, float* m, float* l,
                                float* n, void* out, int out_type, hipStream_t stream) {
-  const uint64_t want = 2ull * device_cus();
+  const uint64_t want = kSliceGroupsWanted;
   const dim3 block(kSliceThreads);
   if (uint64_t(row_heads) * (D / 64) >= want)
     hipLaunchKernelGGL((merge_slices_kernel<D, 64>), dim3(row_heads, D / 64), block, 0, stream, splits, scratch,

@@ -310,20 +310,19 @@ void oracle_fixture(uint32_t tokens, int permute, float* q, int64_t* qpos, int64
   }
 }
 
+/* scale = absmax / 127 (1 for an all-zero row), code = clamp(rint(x / scale),
+ * -127, 127), in fp32 with IEEE maxNum / minNum (fmaxf / fminf) for the max
+ * and the clamp: NaN elements are left out of the absmax, an infinite element
+ * makes the scale infinite, and a NaN quotient clamps to -127. */
 static void quantize_row(const float* x, uint32_t dim, int8_t* code, float* scale) {
   float amax = 0.0f;
-  for (uint32_t d = 0; d < dim; ++d) {
-    const float a = fabsf(x[d]);
-    if (a > amax) amax = a;
-  }
+  for (uint32_t d = 0; d < dim; ++d) amax = fmaxf(amax, fabsf(x[d]));
   const float div = g_fault == ORACLE_FAULT_QUANT_SCALE_128 ? 128.0f : 127.0f;
   const float sc = amax == 0.0f ? 1.0f : amax / div;
   for (uint32_t d = 0; d < dim; ++d) {
     const float q = x[d] / sc;
-    float r = g_fault == ORACLE_FAULT_QUANT_ROUND_AWAY ? roundf(q) : rintf(q);
-    if (r > 127.0f) r = 127.0f;
-    if (r < -127.0f) r = -127.0f;
-    code[d] = (int8_t)r;
+    const float r = g_fault == ORACLE_FAULT_QUANT_ROUND_AWAY ? roundf(q) : rintf(q);
+    code[d] = (int8_t)fminf(fmaxf(r, -127.0f), 127.0f);
   }
   *scale = sc;
 }

@@ -83,3 +83,53 @@ def test_planted_mistakes_are_caught(fault):
     finally:
         O.set_fault(0)
     assert not all(np.array_equal(g, w) for g, w in zip(got, want)), fault
+
+
+def numpy_quantize_nonfinite(x):
+    """Independent formulation of the rule for any fp32 rows: absmax by
+    np.fmax (NaN left out), scale = absmax / 127 (1 for 0), code =
+    fmin(fmax(rint(x / scale), -127), 127) with fmax / fmin NaN-ignoring, so a
+    NaN quotient gives -127."""
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+        absmax = np.fmax.reduce(np.abs(x), axis=-1, initial=np.float32(0)).astype(np.float32)
+        scale = np.where(absmax == 0, np.float32(1), (absmax / np.float32(127)).astype(np.float32))
+        q = (x / scale[..., None]).astype(np.float32)
+        code = np.fmin(np.fmax(np.rint(q), np.float32(-127)), np.float32(127)).astype(np.int8)
+    return code, scale
+
+
+def test_non_finite_known_answers():
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    pool = empty_pool(1, 1, 4, 4)
+    kn = np.array([[[nan, 1.0, -2.0, 0.5]],     # NaN left out of the absmax: scale 2/127, NaN -> -127
+                   [[inf, 1.0, -3.0, -inf]],    # infinite scale: finite -> 0, +-inf (inf/inf = NaN) -> -127
+                   [[nan, nan, nan, nan]]],     # absmax 0: scale 1, every code -127
+                  np.float32)
+    vn = np.zeros_like(kn)
+    k, v, ks, vs = O.append_int8(*pool, kn, vn, np.array([0, 1, 2], np.uint32), 4)
+    assert k[0, 0, 0].tolist() == [-127, 64, -127, 32] and ks[0, 0, 0] == np.float32(2) / np.float32(127)
+    assert k[0, 0, 1].tolist() == [-127, 0, 0, -127] and np.isposinf(ks[0, 0, 1])
+    assert k[0, 0, 2].tolist() == [-127] * 4 and ks[0, 0, 2] == 1.0
+    assert vs[0, 0, :3].tolist() == [1.0, 1.0, 1.0]
+
+
+def test_non_finite_matches_numpy_formulation():
+    rng = np.random.default_rng(11)
+    tokens, kvh, D, P = 64, 2, 96, 16
+    pool = empty_pool(5, kvh, P, D)
+    kn = rng.standard_normal((tokens, kvh, D), dtype=np.float32)
+    vn = rng.standard_normal((tokens, kvh, D), dtype=np.float32)
+    for a in (kn, vn):
+        hit = rng.random(a.shape) < 0.02
+        a[hit] = rng.choice(np.array([np.nan, np.inf, -np.inf], np.float32), hit.sum())
+    kn[5, 1] = np.nan
+    vn[7, 0, :] = np.inf
+    slots = rng.permutation(5 * P)[:tokens].astype(np.uint32)
+    k, v, ks, vs = O.append_int8(*pool, kn, vn, slots, P)
+    kc, kscale = numpy_quantize_nonfinite(kn)
+    vc, vscale = numpy_quantize_nonfinite(vn)
+    for t, sid in enumerate(slots):
+        page, slot = divmod(int(sid), P)
+        assert np.array_equal(k[page, :, slot, :], kc[t]) and np.array_equal(v[page, :, :, slot], vc[t])
+        assert np.array_equal(ks[page, :, slot].view(np.uint32), kscale[t].view(np.uint32))
+        assert np.array_equal(vs[page, :, slot].view(np.uint32), vscale[t].view(np.uint32))

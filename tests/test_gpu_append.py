@@ -160,6 +160,54 @@ def test_append_near_ties_matches_oracle_bitwise(gpu, case):
                               w.view(np.uint8) if w.dtype == np.int8 else w.view(np.uint32)), f"{name} differs"
 
 
+NON_FINITE_CASES = [
+    # tokens, kv_heads, dim, page, src: the row, tile and row-streaming kernels
+    (5, 4, 128, 64, kvb.KVB_SRC_F32),
+    (5, 4, 128, 64, kvb.KVB_SRC_F16),
+    (300, 3, 67, 32, kvb.KVB_SRC_F32),
+    (300, 3, 67, 32, kvb.KVB_SRC_F16),
+    (320, 4, 128, 64, kvb.KVB_SRC_F32),
+    (320, 4, 128, 64, kvb.KVB_SRC_F16),
+]
+
+
+@pytest.mark.parametrize("case", NON_FINITE_CASES)
+def test_append_non_finite_sources_match_oracle_bitwise(gpu, case):
+    """Rows holding NaN and +-infinity: every kernel follows the one rule of
+    the oracle (NaN left out of the absmax, an infinite element makes the
+    scale infinite, a NaN quotient clamps to -127), bitwise."""
+    import torch
+
+    tokens, kvh, D, P, src = case
+    rng = np.random.default_rng(tokens * 17 + D + src)
+    pages = -(-tokens // P) + 1
+    slots = rng.permutation(pages * P)[:tokens].astype(np.uint32)
+    tdt = getattr(torch, SRC[src])
+    bufs = []
+    for _ in range(2):
+        x = rng.standard_normal((tokens, kvh, D), dtype=np.float32) * 2
+        hit = rng.random(x.shape) < 0.01
+        x[hit] = rng.choice(np.array([np.nan, np.inf, -np.inf], np.float32), hit.sum())
+        x[1, 0, 3] = np.nan                        # a NaN in an otherwise finite row
+        x[2, 0, 5] = np.inf                        # an infinite element: infinite scale
+        x[3, 0, :] = np.nan                        # an all-NaN row: scale 1, codes -127
+        bufs.append(torch.from_numpy(x.reshape(tokens, kvh * D)).to(tdt))
+    kbuf, vbuf = bufs
+    pool = random_pool(pages, kvh, P, D, seed=tokens)
+    kn = kbuf.float().numpy().reshape(tokens, kvh, D)
+    vn = vbuf.float().numpy().reshape(tokens, kvh, D)
+    want = O.append_int8(*pool, kn, vn, slots, P)
+    dev = [torch.from_numpy(np.ascontiguousarray(a)).to(gpu) for a in pool]
+    s = kvb.append_shape(tokens, kvh, D, P, pages, src)
+    log(f"non-finite append tokens={tokens} kv={kvh} dim={D} page={P} src={SRC[src]}")
+    kvb.append_kv(s, kbuf.to(gpu), vbuf.to(gpu), torch.from_numpy(slots.view(np.int32)).to(gpu), *dev)
+    torch.cuda.synchronize()
+    for name, g, w in zip(("k", "v", "k_scales", "v_scales"), dev, want):
+        got = g.cpu().numpy()
+        assert np.array_equal(got.view(np.uint8) if got.dtype == np.int8 else got.view(np.uint32),
+                              w.view(np.uint8) if w.dtype == np.int8 else w.view(np.uint32)), f"{name} differs"
+
+
 def test_cache_written_by_append_decodes(gpu):
     """Prefill a cfg2-shaped (shorter) cache through three append calls; it
     equals the synthetic generator's cache bitwise and decodes to FP64."""

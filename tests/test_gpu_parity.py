@@ -144,6 +144,9 @@ I8_ROWS_SHAPES = [
     (1, 18, 1, 256, 64, 777, 0, 777, 128, "causal", 0.0),      # 18 head-rows, one kv head, ragged tail
     (6, 40, 5, 256, 16, 3000, 128, 2900, 1024, "masked", 0.01),  # 48 head-rows, 16-token pages, masked rows
     (8, 24, 4, 256, 32, 40000, 0, 39900, 256, "causal", 0.0),  # 156 splits x 4 kv: two per work-group, ragged end
+    # one split of 1,094 tiles: past the 1,024-tile cap of a scale epoch (the
+    # int32 digit-sum bound), and longer than 65,536 tokens
+    (8, 24, 4, 256, 32, 70000, 0, 70000, 70016, "causal", 0.0),
 ]
 
 
