@@ -44,7 +44,8 @@ void decode_attention(const Shape&, const DeviceInput&, unsigned split_tokens,
 // Each sequence runs max(1, ceil(T_b / split_tokens)) splits; the partial
 // stride per sequence is batch_split_count (the split count of max_tokens),
 // and splits past a sequence's own count hold empty partials (two-launch
-// path; the single launch leaves those scratch rows untouched).  The device
+// path; the single launch leaves them untouched and packs its own partials
+// in an internal layout of the same size).  The device
 // metadata is read by the kernels (the call is graph-capturable with
 // changing lengths); indices are clamped to total_tokens / table_entries and
 // T_b to max_tokens, so a malformed batch cannot read out of bounds.

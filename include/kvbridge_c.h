@@ -112,7 +112,10 @@ int kvb_decode_attention(const kvb_shape* s, const kvb_device_input* in, uint32_
  * before the first call; every call leaves them zero (allocate and zero them
  * once, e.g. next to the scratch buffer).  Calls sharing `counters` must not
  * overlap in time (same rule as for scratch).  m, l, n, out equal those of
- * kvb_decode_attention up to fp32 summation order in the merge. */
+ * kvb_decode_attention up to fp32 summation order in the merge.  What the
+ * single launch leaves in scratch is internal: where its merge takes the
+ * short path (<= 32 splits) the partials are packed in a layout of their
+ * own, not the rows kvb_split_attention writes. */
 int kvb_decode_attention_fused(const kvb_shape* s, const kvb_device_input* in, uint32_t split_tokens,
                                float* scratch, uint32_t* counters, float* m, float* l, float* n, void* out,
                                int out_type, void* stream);
@@ -163,7 +166,8 @@ int kvb_batch_output_scalar_elements(const kvb_batch_shape* s, size_t* elements)
  * for kvb_decode_attention_fused), the last work-group of each
  * (sequence, kv head) merging its splits; otherwise two launches.  The
  * single launch writes partials only for each sequence's own splits (the
- * rest of its scratch rows are left as they were). */
+ * rest of that sequence's scratch block is left as it was), in the internal
+ * layout of kvb_decode_attention_fused. */
 int kvb_decode_attention_batched(const kvb_batch_shape* s, const kvb_batch_input* in, float* scratch,
                                  uint32_t* counters, float* m, float* l, float* n, void* out, int out_type,
                                  void* stream);

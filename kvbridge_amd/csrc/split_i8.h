@@ -36,7 +36,9 @@
 // Partial layout and semantics are those of every split kernel here:
 // scratch[((row*q_heads + head)*splits + split)*(dim+2) + col], col 0 = split
 // max score (natural log units), 1 = sum of exp(score - max), 2.. =
-// sum of exp(score - max) * v_scale * v_code.
+// sum of exp(score - max) * v_scale * v_code -- except in the single launch
+// whose merge takes the short path, which packs the same values differently
+// in the same scratch (PackedPartials below).
 #pragma once
 #include <cstdint>
 
@@ -220,6 +222,38 @@ __device__ __forceinline__ float ld_agent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The single launch's short merge (at most 32 splits, one output column per
+// thread) reads a packed partial layout of its own instead of the
+// [row-head][split][m, l, n] rows above (same size, internal to the call):
+//   m: scratch[rh*splits + j]             (RS = rows * q_heads * splits)
+//   l: scratch[RS + rh*splits + j]
+//   n: scratch[2*RS + (rh*splits + j)*D + d]
+// so the merger's (m_j, l_j) of one row-head are one 128-byte line each
+// instead of a line per split, and every 256-byte numerator request of a
+// wave covers two whole 128-byte lines (numerator rows start 512-byte apart,
+// at a 128-byte boundary when the scratch base has one) instead of three.
+// The merge is bound by those line requests: agent-scope loads miss the
+// L2, and one work-group issues all of them.
+template <int D>
+struct PackedPartials {
+  const size_t rs;
+  float* base;
+  __device__ __forceinline__ PackedPartials(float* scratch, const SplitArgs& a)
+      : rs(size_t(a.rows) * a.q_heads * a.splits), base(scratch) {}
+  __device__ __forceinline__ float* m(size_t rh, uint32_t splits, uint32_t j) const { return base + rh * splits + j; }
+  __device__ __forceinline__ float* l(size_t rh, uint32_t splits, uint32_t j) const { return base + rs + rh * splits + j; }
+  __device__ __forceinline__ float* n(size_t rh, uint32_t splits, uint32_t j) const {
+    return base + 2 * rs + (rh * splits + j) * D;
+  }
+};
+
+// Whether the single launch's merge takes the short path (and so the packed
+// layout): every work-group of the kernel evaluates the same condition.
+template <int D, int NW>
+__device__ __forceinline__ bool short_merge(uint32_t ns, uint32_t head_rows) {
+  return ns <= 32u && head_rows * uint32_t(D) <= 64u * NW;
+}
+
 // Merge of all splits of one kv head's head-rows, by the last work-group,
 // with the reference merge semantics (src/attention_shared.cu:295-335):
 // M = max_j m_j; L = sum_{l_j > 0} e^{m_j - M} l_j; N[d] likewise (N summed
@@ -238,27 +272,30 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
   auto row_head = [&](uint32_t hh) __attribute__((always_inline)) {
     return size_t(hh / a.group) * a.q_heads + kv * a.group + hh % a.group;
   };
-  // Common case (<= 32 splits, one output per thread): straight-line code
-  // that requests every operand at once -- the wave's (m_j, l_j) and the
-  // thread's 32 numerators, split indices clamped instead of branched on --
-  // so the merge costs one memory round trip.  The 64 outputs of a wave lie
-  // in one head-row (64 divides D), so every wave turns its own head-row's
-  // (m_j, l_j) into the factors e^{m_j - M} (lane j holds split j) and reads
-  // them back with readlane: no LDS exchange and no work-group barrier.
-  if (ns <= kCh && outs <= 64u * NW) {
+  // Common case (<= 32 splits, one output per thread; the packed partial
+  // layout): straight-line code that requests every operand at once -- the
+  // wave's (m_j, l_j) and the thread's 32 numerators, split indices clamped
+  // instead of branched on -- so the merge costs one memory round trip.  The
+  // 64 outputs of a wave lie in one head-row (64 divides D), so every wave
+  // turns its own head-row's (m_j, l_j) into the factors e^{m_j - M} (lane j
+  // holds split j) and reads them back with readlane: no LDS exchange and no
+  // work-group barrier.
+  if (short_merge<D, NW>(ns, head_rows)) {
     static_assert(D % 64 == 0, "a wave's outputs lie in one head-row");
+    static_assert(kCh == 32, "the short merge covers 32 splits");
     if (64u * wave >= outs) return;
     const uint32_t jmax = ns - 1u;
     const uint32_t hh = (64u * wave) / D;
-    const float* fb = scratch + row_head(hh) * a.splits * W;
+    const PackedPartials<D> pp(const_cast<float*>(scratch), a);
+    const size_t rhh = row_head(hh);
     const uint32_t jl = lane < ns ? lane : jmax;
-    const float mj = ld_agent(fb + size_t(jl) * W);
-    const float lj = ld_agent(fb + size_t(jl) * W + 1);
+    const float mj = ld_agent(pp.m(rhh, a.splits, jl));
+    const float lj = ld_agent(pp.l(rhh, a.splits, jl));
     const uint32_t d = tid % D;
-    const float* nb = fb + 2 + d;
+    const float* nb = pp.n(rhh, a.splits, 0) + d;
     float pre[kCh];
 #pragma unroll
-    for (uint32_t j = 0; j < kCh; ++j) pre[j] = ld_agent(nb + size_t(j < jmax ? j : jmax) * W);
+    for (uint32_t j = 0; j < kCh; ++j) pre[j] = ld_agent(nb + size_t(j < jmax ? j : jmax) * D);
     const bool in = lane < ns;
     const float mx = wave_max(in ? mj : neg_inf());
     const float f = in && lj > 0.f ? exp_e(mj - mx) : 0.f;
@@ -917,12 +954,18 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
       lsum = fmaf(f, lv[w], lsum);
     }
     const uint32_t row2 = hh / a.group, head2 = kv * a.group + hh % a.group;
-    float* const dst = scratch + ((size_t(row2) * a.q_heads + head2) * a.splits + split) * W;
-    if constexpr (FUSED) {  // agent-coherent
-      __hip_atomic_store(dst + 2 + d, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const size_t rh = size_t(row2) * a.q_heads + head2;
+    float* const dst = scratch + (rh * a.splits + split) * W;
+    if constexpr (FUSED) {  // agent-coherent; the short merge's packed layout or the rows
+      const bool packed = short_merge<D, NW>(nsplit, head_rows);
+      const PackedPartials<D> pp(scratch, a);
+      float* const pn = packed ? pp.n(rh, a.splits, split) : dst + 2;
+      float* const pm = packed ? pp.m(rh, a.splits, split) : dst;
+      float* const pl = packed ? pp.l(rh, a.splits, split) : dst + 1;
+      __hip_atomic_store(pn + d, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (d == 0) {
-        __hip_atomic_store(dst, mm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(dst + 1, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pm, mm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pl, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     } else {
       dst[2 + d] = val;
