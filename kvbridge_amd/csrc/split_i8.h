@@ -267,7 +267,7 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
                                             const float* __restrict__ scratch, float* f_s, float* ml_s) {
   constexpr uint32_t W = D + 2;
   constexpr uint32_t kCh = 32;  // splits per pass
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t outs = head_rows * D;
   auto row_head = [&](uint32_t hh) __attribute__((always_inline)) {
     return size_t(hh / a.group) * a.q_heads + kv * a.group + hh % a.group;
@@ -292,6 +292,10 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
     const float mj = ld_agent(pp.m(rhh, a.splits, jl));
     const float lj = ld_agent(pp.l(rhh, a.splits, jl));
     const uint32_t d = tid % D;
+    // Numerator j of column d through one descriptor over the head-row's
+    // numerator rows, with the row offset in the instruction's scalar offset
+    // (no per-load vector address arithmetic); agent-coherent cache policy.
+    // Rows past ns - 1 re-read row ns - 1 and are masked below.
     const float* nb = pp.n(rhh, a.splits, 0) + d;
     float pre[kCh];
 #pragma unroll
@@ -300,12 +304,30 @@ __device__ __forceinline__ void fused_merge(const SplitArgs& a, uint32_t kv, uin
     const float mx = wave_max(in ? mj : neg_inf());
     const float f = in && lj > 0.f ? exp_e(mj - mx) : 0.f;
     const float lsum = wave_sum(f * lj);
-    float nacc = 0.f;
+    // The factors reach every lane as LDS broadcasts (this wave's own 32
+    // floats of f_s), and the 32 products go into four interleaved sums
+    // added as (s0 + s1) + (s2 + s3): a fixed order, four times shorter
+    // dependency chains.
+    float* const fw = f_s + wave * kCh;
+    if (lane < kCh) fw[lane] = f;
+    float fv[kCh];
 #pragma unroll
-    for (uint32_t j = 0; j < kCh; ++j) {
-      const float fj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), int(j)));
-      nacc = fmaf(fj, j <= jmax ? pre[j] : 0.f, nacc);
+    for (uint32_t q4 = 0; q4 < kCh / 4u; ++q4) {
+      const float4 x = reinterpret_cast<const float4*>(fw)[q4];
+      fv[4 * q4] = x.x;
+      fv[4 * q4 + 1] = x.y;
+      fv[4 * q4 + 2] = x.z;
+      fv[4 * q4 + 3] = x.w;
     }
+    float s4[4] = {0.f, 0.f, 0.f, 0.f};
+    if (ns == kCh) {
+#pragma unroll
+      for (uint32_t j = 0; j < kCh; ++j) s4[j & 3u] = fmaf(fv[j], pre[j], s4[j & 3u]);
+    } else {
+#pragma unroll
+      for (uint32_t j = 0; j < kCh; ++j) s4[j & 3u] = fmaf(fv[j], j <= jmax ? pre[j] : 0.f, s4[j & 3u]);
+    }
+    const float nacc = (s4[0] + s4[1]) + (s4[2] + s4[3]);
     const size_t rh = row_head(hh);
     if (d == 0) {
       a.m[rh] = mx;
@@ -935,21 +957,27 @@ __global__ __launch_bounds__(64 * NW) void split_i8_kernel(
   // writes the head-row's maximum and denominator.
   constexpr uint32_t W = D + 2;
   for (uint32_t o = threadIdx.x; o < head_rows * uint32_t(D); o += 64u * NW) {
-    const uint32_t hh = o / D, d = o % D;
+    // A wave's 64 columns lie in one head-row (64 divides D), so the NW
+    // wave maxima, denominators and factors of its iteration are scalars:
+    // lane w < NW reads wave w's pair and computes its factor once.
+    const uint32_t hh = __builtin_amdgcn_readfirstlane(o / D), d = o % D;
+    const uint32_t wl = lane < uint32_t(NW) ? lane : 0u;
+    const float m_l = wm_s[wl * HS + hh], l_l = wl_s[wl * HS + hh];
     float mw[NW], lv[NW], xw[NW];
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      mw[w] = wm_s[w * HS + hh];
-      lv[w] = wl_s[w * HS + hh];
+      mw[w] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_l), w));
+      lv[w] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l_l), w));
       xw[w] = wacc_s[(w * HS + hh) * D + d];
     }
     float mm = mw[0];
 #pragma unroll
     for (int w = 1; w < NW; ++w) mm = fmaxf(mm, mw[w]);
+    const float f_l = m_l == neg_inf() ? 0.f : exp_e(m_l - mm);
     float val = 0.f, lsum = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const float f = mw[w] == neg_inf() ? 0.f : exp_e(mw[w] - mm);
+      const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f_l), w));
       val = fmaf(f, xw[w], val);
       lsum = fmaf(f, lv[w], lsum);
     }
