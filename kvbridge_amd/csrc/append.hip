@@ -295,7 +295,7 @@ __global__ __launch_bounds__(64 * kWaves) void append_tile_kernel(AppendArgs a) 
 // each: one coalesced pass, every row read once), the row absmax is an xor
 // shuffle over those lanes, and K codes go out as each lane's contiguous
 // 16 / sizeof(T) bytes of the token's row.  V codes are transposed through
-// LDS ([dim][64 tokens]) and stored 16 tokens per 16-byte store where those
+// LDS ([dim][64 tokens], 68-byte rows) and stored 16 tokens per 16-byte store where those
 // 16 tokens fill 16 consecutive slots of one page starting on a 16-slot
 // boundary (a prefill chunk); any other group of 16 is stored byte by byte.
 // The pool stores are non-temporal (streaming): the codes are not read again
@@ -308,7 +308,11 @@ __global__ __launch_bounds__(64 * kWaves) void append_stream_kernel(AppendArgs a
   constexpr uint32_t LPR = D / EPL;         // lanes per row
   static_assert(LPR >= 4 && LPR <= 64 && 64 % LPR == 0, "row split");
   constexpr uint32_t RPL = 64 / LPR;        // rows per wave-load
-  __shared__ __attribute__((aligned(16))) uint8_t vt[D * 64];  // V codes [d][token]
+  // V codes [d][token] with 68-byte rows: a lane's eight code bytes go to
+  // eight dim rows, and the 16 lanes of a token row hit eight different LDS
+  // banks two by two (64-byte rows put all 16 on one bank).
+  constexpr uint32_t VR = 68;
+  __shared__ __attribute__((aligned(16))) uint8_t vt[D * VR];
   __shared__ uint32_t ids[64];
   __shared__ uint32_t grp_ok[4];
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -361,7 +365,7 @@ __global__ __launch_bounds__(64 * kWaves) void append_stream_kernel(AppendArgs a
       kw[e] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(tk[4 * e + 3], tk[4 * e + 2], 0x0c0c0400u),
                                     __builtin_amdgcn_perm(tk[4 * e + 1], tk[4 * e], 0x0c0c0400u), 0x05040100u);
 #pragma unroll
-    for (uint32_t e = 0; e < EPL; ++e) vt[(e0 + e) * 64u + r] = uint8_t(tv[e]);
+    for (uint32_t e = 0; e < EPL; ++e) vt[(e0 + e) * VR + r] = uint8_t(tv[e]);
     if (id < cap) {
       const size_t row = (size_t(page_of(id)) * a.kv_heads + kv) * P + slot_of(id);
       int8_t* const kdst = a.k + row * D + e0;
@@ -377,11 +381,12 @@ __global__ __launch_bounds__(64 * kWaves) void append_stream_kernel(AppendArgs a
   // V: item (d, group q) of D * 4, two per thread at D = 128.
   for (uint32_t it = threadIdx.x; it < D * 4u; it += 64u * kWaves) {
     const uint32_t d = it >> 2, q = it & 3u;
-    const uint8_t* const src = vt + d * 64u + 16u * q;
+    const uint8_t* const src = vt + d * VR + 16u * q;
     if (grp_ok[q]) {
       const uint32_t id = ids[16u * q];
       int8_t* const dst = a.v + (size_t(page_of(id)) * a.kv_heads + kv) * D * P + size_t(d) * P + slot_of(id);
-      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(src), reinterpret_cast<u32x4*>(dst));
+      const uint32_t* const s4 = reinterpret_cast<const uint32_t*>(src);  // 4-byte aligned rows
+      __builtin_nontemporal_store(u32x4{s4[0], s4[1], s4[2], s4[3]}, reinterpret_cast<u32x4*>(dst));
     } else {
 #pragma unroll 4
       for (uint32_t j = 0; j < 16u; ++j) {
