@@ -72,6 +72,19 @@ __device__ __forceinline__ int8_t quantize(float x, float scale) {
 
 constexpr float kRoundMagic = 12582912.f;  // 1.5 * 2^23
 
+// The per-token scale absmax / 127 (1 for an all-zero row), bitwise the IEEE
+// fp32 quotient: for finite absmax, q0 = RN(a * RN(1/127)) is within an ulp
+// and one residual step fma(fma(-q0, 127, a), RN(1/127), q0) gives the
+// correctly rounded quotient -- checked for every non-negative finite fp32
+// value by tests/cpp/scale_div_check.c -- in three instructions instead of
+// the division sequence.  An infinite absmax keeps the quotient (infinity).
+__device__ __forceinline__ float scale_of(float amax) {
+  constexpr float kInv127 = 1.0f / 127.0f;
+  const float q0 = __fmul_rn(amax, kInv127);
+  const float q = fmaf(fmaf(-q0, 127.f, amax), kInv127, q0);
+  return amax == 0.f ? 1.f : (amax <= 3.4028234663852886e38f ? q : amax);
+}
+
 // |x| max of the N elements of type T in a 16-byte word (exact: max picks
 // an element), NaN elements ignored like fmaxf does (as in the row and tile
 // kernels).  fp16: the sign bits cleared, non-NaN halves order like their
@@ -163,7 +176,7 @@ __device__ __forceinline__ void quantize_row(const T* __restrict__ src, uint32_t
     amax = fmaxf(amax, fabsf(x[i]));
   }
   amax = wave_max(amax);
-  scale = amax == 0.f ? 1.f : amax / 127.f;
+  scale = scale_of(amax);
 #pragma unroll
   for (int i = 0; i < 4; ++i) code[i] = quantize(x[i], scale);
 }
@@ -257,8 +270,8 @@ __global__ __launch_bounds__(64 * kWaves) void append_tile_kernel(AppendArgs a) 
     kamax = fmaxf(kamax, amax_s[0][w][lane]);
     vamax = fmaxf(vamax, amax_s[1][w][lane]);
   }
-  const float ks = kamax == 0.f ? 1.f : kamax / 127.f;
-  const float vs = vamax == 0.f ? 1.f : vamax / 127.f;
+  const float ks = scale_of(kamax);
+  const float vs = scale_of(vamax);
   const size_t row = (size_t(id / P) * a.kv_heads + kv) * P + id % P;  // token row of this (page, kv)
   if (wave == 0) {
     a.k_scales[row] = ks;
@@ -290,8 +303,8 @@ __global__ __launch_bounds__(64 * kWaves) void append_tile_kernel(AppendArgs a) 
 }
 
 // append_stream_kernel (prefill-sized appends from 16-byte aligned rows, dim
-// 64/128/256): one work-group of four waves per (64 new tokens, kv head).
-// Wave w loads tokens 16w .. 16w + 15 row-major (LPR lanes per row, 16 bytes
+// 64/128/256): one work-group of eight waves per (64 new tokens, kv head).
+// Wave w loads tokens 8w .. 8w + 7 row-major (LPR lanes per row, 16 bytes
 // each: one coalesced pass, every row read once), the row absmax is an xor
 // shuffle over those lanes, and K codes go out as each lane's contiguous
 // 16 / sizeof(T) bytes of the token's row.  V codes are transposed through
@@ -302,8 +315,13 @@ __global__ __launch_bounds__(64 * kWaves) void append_tile_kernel(AppendArgs a) 
 // by this launch, and cached write-back stores measured slower (4,096 /
 // 16,384 / 65,536 tokens at d128: 8.2 / 23.2 / 86.8 us against 7.9 / 21.9 /
 // 69.4 us).  The source loads stay cached: non-temporal loads were slower.
+// Eight waves of eight tokens rather than four of sixteen: the work-group's
+// arithmetic (absmax, scale, codes) is a dependent chain per token row, and
+// twice the waves per SIMD hide each other's latency (4,096 tokens at d128:
+// 6.54 against 7.21 us).
+constexpr int kStreamWaves = 8;
 template <class T, int D, bool P2>  // P2: page_tokens is a power of two
-__global__ __launch_bounds__(64 * kWaves) void append_stream_kernel(AppendArgs a) {
+__global__ __launch_bounds__(64 * kStreamWaves) void append_stream_kernel(AppendArgs a) {
   constexpr uint32_t EPL = 16 / sizeof(T);  // elements per lane per load
   constexpr uint32_t LPR = D / EPL;         // lanes per row
   static_assert(LPR >= 4 && LPR <= 64 && 64 % LPR == 0, "row split");
@@ -321,14 +339,16 @@ __global__ __launch_bounds__(64 * kWaves) void append_stream_kernel(AppendArgs a
   const uint32_t psh = __builtin_ctz(P);
   auto page_of = [&](uint32_t id) { return P2 ? id >> psh : id / P; };
   auto slot_of = [&](uint32_t id) { return P2 ? id & (P - 1u) : id % P; };
-  constexpr uint32_t NI = 16u / RPL;  // row slices per lane
+  constexpr uint32_t TPW = 64u / kStreamWaves;  // tokens per wave
+  static_assert(TPW % RPL == 0, "a wave's tokens fill whole row slices");
+  constexpr uint32_t NI = TPW / RPL;  // row slices per lane
   const uint32_t sub = lane % LPR, e0 = sub * EPL;
   // Every source load of the wave first (they do not depend on the slot
   // ids), so they are all in flight together; then the slot ids.
   u32x4 wk[NI], wv[NI];
 #pragma unroll
   for (uint32_t i = 0; i < NI; ++i) {
-    const uint32_t t = t0 + 16u * wave + RPL * i + lane / LPR;
+    const uint32_t t = t0 + TPW * wave + RPL * i + lane / LPR;
     if (t < a.tokens) {
       wk[i] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k_new) + size_t(t) * a.k_stride +
                                               size_t(kv) * D + e0);
@@ -350,12 +370,12 @@ __global__ __launch_bounds__(64 * kWaves) void append_stream_kernel(AppendArgs a
   __syncthreads();
 #pragma unroll
   for (uint32_t i = 0; i < NI; ++i) {
-    const uint32_t r = 16u * wave + RPL * i + lane / LPR;  // token of the tile
+    const uint32_t r = TPW * wave + RPL * i + lane / LPR;  // token of the tile
     const uint32_t id = ids[r];
     const float ka = group_max<LPR>(word_absmax<T, EPL>(wk[i]));  // the row's lanes are an aligned group
     const float va = group_max<LPR>(word_absmax<T, EPL>(wv[i]));
-    const float ks = ka == 0.f ? 1.f : ka / 127.f;
-    const float vs = va == 0.f ? 1.f : va / 127.f;
+    const float ks = scale_of(ka);
+    const float vs = scale_of(va);
     uint32_t tk[EPL], tv[EPL];
     quantize_word<T, EPL>(wk[i], ks, tk);
     quantize_word<T, EPL>(wv[i], vs, tv);
@@ -378,8 +398,8 @@ __global__ __launch_bounds__(64 * kWaves) void append_stream_kernel(AppendArgs a
     }
   }
   __syncthreads();
-  // V: item (d, group q) of D * 4, two per thread at D = 128.
-  for (uint32_t it = threadIdx.x; it < D * 4u; it += 64u * kWaves) {
+  // V: item (d, group q) of D * 4, one per thread at D = 128.
+  for (uint32_t it = threadIdx.x; it < D * 4u; it += 64u * kStreamWaves) {
     const uint32_t d = it >> 2, q = it & 3u;
     const uint8_t* const src = vt + d * VR + 16u * q;
     if (grp_ok[q]) {
@@ -419,8 +439,8 @@ hipError_t launch_typed(const AppendArgs& a, hipStream_t stream) {
     const bool p2 = (a.page_tokens & (a.page_tokens - 1u)) == 0u;
     auto go = [&](auto dc) {
       constexpr int DD = decltype(dc)::value;
-      if (p2) hipLaunchKernelGGL((append_stream_kernel<T, DD, true>), sgrid, dim3(64 * kWaves), 0, stream, a);
-      else hipLaunchKernelGGL((append_stream_kernel<T, DD, false>), sgrid, dim3(64 * kWaves), 0, stream, a);
+      if (p2) hipLaunchKernelGGL((append_stream_kernel<T, DD, true>), sgrid, dim3(64 * kStreamWaves), 0, stream, a);
+      else hipLaunchKernelGGL((append_stream_kernel<T, DD, false>), sgrid, dim3(64 * kStreamWaves), 0, stream, a);
     };
     if (a.dim == 64) { go(std::integral_constant<int, 64>{}); return hipGetLastError(); }
     if (a.dim == 128) { go(std::integral_constant<int, 128>{}); return hipGetLastError(); }

@@ -133,3 +133,23 @@ def test_non_finite_matches_numpy_formulation():
         assert np.array_equal(k[page, :, slot, :], kc[t]) and np.array_equal(v[page, :, :, slot], vc[t])
         assert np.array_equal(ks[page, :, slot].view(np.uint32), kscale[t].view(np.uint32))
         assert np.array_equal(vs[page, :, slot].view(np.uint32), vscale[t].view(np.uint32))
+
+
+def test_fast_scale_division_is_the_ieee_quotient():
+    """The append kernels compute absmax / 127 as q0 = RN(a * RN(1/127)) plus
+    one fma residual step (append.hip scale_of).  tests/cpp/scale_div_check.c
+    compares it bitwise with IEEE single division on every 61st non-negative
+    finite fp32 bit pattern and on every value an fp16 row maximum can take
+    (its full sweep, stride 1, also finds no mismatch).  A planted mistake --
+    the first product alone, without the residual step -- must be caught."""
+    import subprocess
+    from pathlib import Path
+    here = Path(__file__).resolve().parent / "cpp"
+    subprocess.run(["make", "-s", "-C", str(here), "scale_div_check"], check=True)
+    r = subprocess.run([str(here / "scale_div_check")], capture_output=True, text=True)
+    assert r.returncode == 0 and " 0 mismatches" in r.stdout, r.stdout
+    # the planted mistake, restated in numpy: RN(a * RN(1/127)) without the correction
+    rng = np.random.default_rng(5)
+    a = rng.uniform(0, 1e4, 200_000).astype(np.float32)
+    c = np.float32(1) / np.float32(127)
+    assert np.any((a * c) != (a / np.float32(127)))
