@@ -85,81 +85,108 @@ __device__ __forceinline__ float scale_of(float amax) {
   return amax == 0.f ? 1.f : (amax <= 3.4028234663852886e38f ? q : amax);
 }
 
-// |x| max of the N elements of type T in a 16-byte word (exact: max picks
-// an element), NaN elements ignored like fmaxf does (as in the row and tile
-// kernels).  fp16: the sign bits cleared, non-NaN halves order like their
-// 16-bit patterns, so a packed unsigned 16-bit max (two elements an
-// instruction) finds the largest magnitude; a NaN (pattern above infinity's
-// 0x7c00) wins that max, and such a word (rare) is redone element by element.
+// |x| max of the N elements of type T in a 16-byte word, as the bit pattern of
+// a non-negative fp32 value (exact: max picks an element), NaN elements
+// ignored like fmaxf does (as in the row and tile kernels).  Non-negative
+// floats order like their bit patterns, so the maxima are unsigned integer
+// maxima of the patterns with the sign cleared (fp16 / bf16: two elements an
+// instruction); a NaN (pattern above infinity's) wins that max, and such a
+// word (rare) is redone element by element.  nonfinite: the word holds an
+// infinity or a NaN.
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 template <class T, uint32_t N>
-__device__ __forceinline__ float word_absmax(const u32x4& w) {
-  if constexpr (std::is_same<T, _Float16>::value) {
+__device__ __forceinline__ uint32_t word_absmax_bits(const u32x4& w, bool& nonfinite) {
+  const T* e = reinterpret_cast<const T*>(&w);
+  auto slow = [&]() {
+    float a = 0.f;
+#pragma unroll
+    for (uint32_t i = 0; i < N; ++i) a = fmaxf(a, fabsf(to_f32(e[i])));
+    return __float_as_uint(a);
+  };
+  if constexpr (sizeof(T) == 2) {
+    constexpr uint16_t kInf = std::is_same<T, _Float16>::value ? 0x7c00u : 0x7f80u;
     u16x2 m = __builtin_bit_cast(u16x2, w[0] & 0x7fff7fffu);
 #pragma unroll
     for (int j = 1; j < 4; ++j) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[j] & 0x7fff7fffu));
     const uint16_t b = m[0] > m[1] ? m[0] : m[1];
-    if (b <= 0x7c00u) return float(__builtin_bit_cast(_Float16, b));
-    const _Float16* e = reinterpret_cast<const _Float16*>(&w);
-    float a = 0.f;
-#pragma unroll
-    for (uint32_t i = 0; i < N; ++i) a = fmaxf(a, fabsf(float(e[i])));
-    return a;
+    nonfinite = b >= kInf;
+    if (b > kInf) return slow();
+    if constexpr (std::is_same<T, _Float16>::value) return __float_as_uint(float(__builtin_bit_cast(_Float16, b)));
+    else return uint32_t(b) << 16;
   } else {
-    const T* e = reinterpret_cast<const T*>(&w);
-    float a = 0.f;
+    uint32_t m = w[0] & 0x7fffffffu;
 #pragma unroll
-    for (uint32_t i = 0; i < N; ++i) a = fmaxf(a, fabsf(to_f32(e[i])));
-    return a;
+    for (int j = 1; j < 4; ++j) m = max(m, w[j] & 0x7fffffffu);
+    nonfinite = m >= 0x7f800000u;
+    if (m > 0x7f800000u) return slow();
+    return m;
   }
 }
 
-// quantize_slice on the N elements of a 16-byte word: the product with the
-// reciprocal, the rounding add and the check in mixed-precision fmas (fp16
-// elements need no conversion instruction).  t = RN(x * r + 1.5 * 2^23)
-// rounds the exact product x * r to the nearest integer n directly, and
-// d = RN(x * r - n) measures its distance from n; the same 2^-14 margin as
-// quantize() applies (|x * r - x / scale| <= 4e-5).
+// The codes of the N elements of a 16-byte word, quantize() bitwise.  With
+// r the hardware reciprocal of the scale (within one ulp of 1/scale),
+// r_lo = RN(r * (1 - 2^-21)) and r_hi = RN(r * (1 + 2^-21)), the products
+// x * r_lo and x * r_hi bracket the IEEE quotient RN(x / scale); fma(x, r, M)
+// with M = 1.5 * 2^23 rounds the exact product to the nearest integer n
+// (half to even) in the low mantissa bits, and rounding to the nearest
+// integer is monotone, so where both ends give the same n it is
+// rint(RN(x / scale)) -- every fp16 row maximum and source value, and random
+// fp32 rows, are checked by tests/cpp/quant_bracket_check.c.  Where the ends
+// differ (a quotient within ~2^-21 relative of a half-integer, e.g. an exact
+// tie), where the word holds a non-finite element, or where the reciprocal is
+// not finite (force), the word takes the division and the clamp of
+// quantize() (a NaN quotient gives -127).  The ends are compared by a sum of
+// absolute differences of their low 16 bits (the two n differ by at most 1).
 template <class T, uint32_t N>
-__device__ __forceinline__ void quantize_word(const u32x4& w, float scale, uint32_t (&t)[N]) {
+__device__ __forceinline__ void quantize_word(const u32x4& w, float scale, float r_lo, float r_hi, bool force,
+                                              uint32_t (&t)[N]) {
   const T* e = reinterpret_cast<const T*>(&w);
-  const float r = __builtin_amdgcn_rcpf(scale);
-  uint32_t amb = 0u;
+  uint32_t amb = force ? 1u : 0u;
 #pragma unroll
   for (uint32_t i = 0; i < N; ++i) {
     const float x = to_f32(e[i]);
-    const float ti = fmaf(x, r, kRoundMagic);
-    const float d = fmaf(x, r, -(ti - kRoundMagic));
-    amb |= fabsf(d) <= 0.5f - 0x1p-14f ? 0u : 1u;  // NaN counts as near
-    t[i] = __float_as_uint(ti);
+    const float lo = fmaf(x, r_lo, kRoundMagic);
+    const float hi = fmaf(x, r_hi, kRoundMagic);
+    amb = __builtin_amdgcn_sad_u16(__float_as_uint(lo), __float_as_uint(hi), amb);
+    t[i] = __float_as_uint(lo);
   }
-  if (amb != 0u) {  // rare: one branch per word; the clamp of quantize() (a NaN quotient gives -127)
+  if (amb != 0u) {  // rare: one branch per word
 #pragma unroll
     for (uint32_t i = 0; i < N; ++i)
       t[i] = __float_as_uint(fminf(fmaxf(__builtin_rintf(to_f32(e[i]) / scale), -127.f), 127.f) + kRoundMagic);
   }
 }
 
+// The reciprocal bracket of quantize_word for one row's scale; force when the
+// reciprocal is not finite (a scale below the normal range).
+__device__ __forceinline__ void bracket_of(float scale, float& r_lo, float& r_hi, bool& force) {
+  const float r = __builtin_amdgcn_rcpf(scale);
+  r_lo = r * (1.0f - 0x1p-21f);
+  r_hi = r * (1.0f + 0x1p-21f);
+  force = !(r_hi <= 3.4028234663852886e38f);
+}
+
 // Max over aligned groups of L lanes (L a power of two, 4..64), in every lane
-// of the group: DPP quad permutes and row mirrors inside a 16-lane row, then
-// the gfx950 permlane swaps across rows.
+// of the group, of non-negative fp32 bit patterns (unsigned maxima): DPP
+// quad permutes and row mirrors inside a 16-lane row (each folded into one
+// v_max_u32), then the gfx950 permlane swaps across rows.
 template <uint32_t L>
-__device__ __forceinline__ float group_max(float x) {
+__device__ __forceinline__ uint32_t group_max_bits(uint32_t x) {
   static_assert(L >= 4 && L <= 64 && (L & (L - 1)) == 0, "group size");
-  auto dpp = [](float v, auto ctrl) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), decltype(ctrl)::value, 0xF, 0xF, false));
+  auto dpp = [](uint32_t v, auto ctrl) {
+    return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), decltype(ctrl)::value, 0xF, 0xF, false));
   };
-  x = fmaxf(x, dpp(x, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
-  x = fmaxf(x, dpp(x, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
-  if constexpr (L >= 8) x = fmaxf(x, dpp(x, std::integral_constant<int, 0x141>{}));  // row_half_mirror
-  if constexpr (L >= 16) x = fmaxf(x, dpp(x, std::integral_constant<int, 0x140>{}));  // row_mirror
+  x = max(x, dpp(x, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
+  x = max(x, dpp(x, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
+  if constexpr (L >= 8) x = max(x, dpp(x, std::integral_constant<int, 0x141>{}));  // row_half_mirror
+  if constexpr (L >= 16) x = max(x, dpp(x, std::integral_constant<int, 0x140>{}));  // row_mirror
   if constexpr (L >= 32) {
-    auto p = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
-    x = fmaxf(__int_as_float(p[0]), __int_as_float(p[1]));
+    auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    x = max(uint32_t(p[0]), uint32_t(p[1]));
   }
   if constexpr (L >= 64) {
-    auto p = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
-    x = fmaxf(__int_as_float(p[0]), __int_as_float(p[1]));
+    auto p = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    x = max(uint32_t(p[0]), uint32_t(p[1]));
   }
   return x;
 }
@@ -372,13 +399,18 @@ __global__ __launch_bounds__(64 * kStreamWaves) void append_stream_kernel(Append
   for (uint32_t i = 0; i < NI; ++i) {
     const uint32_t r = TPW * wave + RPL * i + lane / LPR;  // token of the tile
     const uint32_t id = ids[r];
-    const float ka = group_max<LPR>(word_absmax<T, EPL>(wk[i]));  // the row's lanes are an aligned group
-    const float va = group_max<LPR>(word_absmax<T, EPL>(wv[i]));
-    const float ks = scale_of(ka);
-    const float vs = scale_of(va);
+    bool knf, vnf;
+    const uint32_t ka = group_max_bits<LPR>(word_absmax_bits<T, EPL>(wk[i], knf));  // the row's lanes are an aligned group
+    const uint32_t va = group_max_bits<LPR>(word_absmax_bits<T, EPL>(wv[i], vnf));
+    const float ks = scale_of(__uint_as_float(ka));
+    const float vs = scale_of(__uint_as_float(va));
+    float klo, khi, vlo, vhi;
+    bool kf, vf;
+    bracket_of(ks, klo, khi, kf);
+    bracket_of(vs, vlo, vhi, vf);
     uint32_t tk[EPL], tv[EPL];
-    quantize_word<T, EPL>(wk[i], ks, tk);
-    quantize_word<T, EPL>(wv[i], vs, tv);
+    quantize_word<T, EPL>(wk[i], ks, klo, khi, kf || knf, tk);
+    quantize_word<T, EPL>(wv[i], vs, vlo, vhi, vf || vnf, tv);
     uint32_t kw[EPL / 4];
 #pragma unroll
     for (uint32_t e = 0; e < EPL / 4; ++e)  // low bytes of four words

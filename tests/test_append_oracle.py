@@ -153,3 +153,26 @@ def test_fast_scale_division_is_the_ieee_quotient():
     a = rng.uniform(0, 1e4, 200_000).astype(np.float32)
     c = np.float32(1) / np.float32(127)
     assert np.any((a * c) != (a / np.float32(127)))
+
+
+def test_bracketed_code_rounding_is_the_ieee_quotient():
+    """The row-streaming append kernel rounds x / scale to its code from two
+    fmas, x * RN(r * (1 -+ 2^-21)) + 1.5 * 2^23 with r the hardware
+    reciprocal, and divides only where the two disagree (append.hip
+    quantize_word).  tests/cpp/quant_bracket_check.c checks that agreement
+    implies rint(RN(x / scale)) for every fp32 r within one ulp of 1/scale,
+    every 5th fp16 row maximum with every fp16 source value below it (both
+    signs), and random fp32 rows including their exact ties (its full fp16
+    sweep, stride 1, also finds no mismatch).  Planted mistakes -- a bracket of
+    2^-23, too narrow for the reciprocal's ulp, and no bracket at all -- must
+    be caught."""
+    import subprocess
+    from pathlib import Path
+    here = Path(__file__).resolve().parent / "cpp"
+    subprocess.run(["make", "-s", "-C", str(here), "quant_bracket_check"], check=True)
+    exe = str(here / "quant_bracket_check")
+    r = subprocess.run([exe], capture_output=True, text=True)
+    assert r.returncode == 0 and " 0 mismatches" in r.stdout, r.stdout
+    for k in ("23", "0"):
+        bad = subprocess.run([exe, "37", "200000", k], capture_output=True, text=True)
+        assert bad.returncode == 1 and " 0 mismatches" not in bad.stdout, (k, bad.stdout)

@@ -113,6 +113,9 @@ NEAR_TIE_CASES = [
     (300, 4, 67, 32, kvb.KVB_SRC_F32),
     (320, 4, 128, 64, kvb.KVB_SRC_F32),
     (320, 4, 128, 64, kvb.KVB_SRC_F16),
+    (320, 4, 128, 64, kvb.KVB_SRC_BF16),
+    (320, 2, 64, 16, kvb.KVB_SRC_F16),
+    (288, 2, 256, 32, kvb.KVB_SRC_F32),
 ]
 
 
@@ -168,6 +171,7 @@ NON_FINITE_CASES = [
     (300, 3, 67, 32, kvb.KVB_SRC_F16),
     (320, 4, 128, 64, kvb.KVB_SRC_F32),
     (320, 4, 128, 64, kvb.KVB_SRC_F16),
+    (320, 4, 128, 64, kvb.KVB_SRC_BF16),
 ]
 
 
@@ -175,7 +179,9 @@ NON_FINITE_CASES = [
 def test_append_non_finite_sources_match_oracle_bitwise(gpu, case):
     """Rows holding NaN and +-infinity: every kernel follows the one rule of
     the oracle (NaN left out of the absmax, an infinite element makes the
-    scale infinite, a NaN quotient clamps to -127), bitwise."""
+    scale infinite, a NaN quotient clamps to -127), bitwise.  One row of
+    subnormal magnitudes (fp32 and bf16 sources) has a scale below the
+    normal range, whose reciprocal the kernels do not use."""
     import torch
 
     tokens, kvh, D, P, src = case
@@ -191,6 +197,7 @@ def test_append_non_finite_sources_match_oracle_bitwise(gpu, case):
         x[1, 0, 3] = np.nan                        # a NaN in an otherwise finite row
         x[2, 0, 5] = np.inf                        # an infinite element: infinite scale
         x[3, 0, :] = np.nan                        # an all-NaN row: scale 1, codes -127
+        x[4, 0, :] = rng.standard_normal(D, dtype=np.float32) * np.float32(1e-39)  # subnormal scale
         bufs.append(torch.from_numpy(x.reshape(tokens, kvh * D)).to(tdt))
     kbuf, vbuf = bufs
     pool = random_pool(pages, kvh, P, D, seed=tokens)
