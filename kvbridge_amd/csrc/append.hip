@@ -85,85 +85,125 @@ __device__ __forceinline__ float scale_of(float amax) {
   return amax == 0.f ? 1.f : (amax <= 3.4028234663852886e38f ? q : amax);
 }
 
-// |x| max of the N elements of type T in a 16-byte word, as the bit pattern of
-// a non-negative fp32 value (exact: max picks an element), NaN elements
-// ignored like fmaxf does (as in the row and tile kernels).  Non-negative
-// floats order like their bit patterns, so the maxima are unsigned integer
-// maxima of the patterns with the sign cleared (fp16 / bf16: two elements an
-// instruction); a NaN (pattern above infinity's) wins that max, and such a
-// word (rare) is redone element by element.  nonfinite: the word holds an
-// infinity or a NaN.
+// |x| max of a lane's W 16-byte words of N elements of type T, as the bit
+// pattern of a non-negative fp32 value (exact: max picks an element), NaN
+// elements ignored like fmaxf does (as in the row and tile kernels).
+// Non-negative floats order like their bit patterns, so the maxima are
+// unsigned integer maxima of the patterns with the sign cleared (fp16 / bf16:
+// two elements an instruction); a NaN (pattern above infinity's) wins that
+// max, and such a lane (rare) is redone element by element.  nonfinite: the
+// words hold an infinity or a NaN.
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
-template <class T, uint32_t N>
-__device__ __forceinline__ uint32_t word_absmax_bits(const u32x4& w, bool& nonfinite) {
-  const T* e = reinterpret_cast<const T*>(&w);
+template <class T, uint32_t N, uint32_t W>
+__device__ __forceinline__ uint32_t lane_absmax_bits(const u32x4 (&w)[W], bool& nonfinite) {
   auto slow = [&]() {
     float a = 0.f;
 #pragma unroll
-    for (uint32_t i = 0; i < N; ++i) a = fmaxf(a, fabsf(to_f32(e[i])));
+    for (uint32_t j = 0; j < W; ++j) {
+      const T* e = reinterpret_cast<const T*>(&w[j]);
+#pragma unroll
+      for (uint32_t i = 0; i < N; ++i) a = fmaxf(a, fabsf(to_f32(e[i])));
+    }
     return __float_as_uint(a);
   };
   if constexpr (sizeof(T) == 2) {
     constexpr uint16_t kInf = std::is_same<T, _Float16>::value ? 0x7c00u : 0x7f80u;
-    u16x2 m = __builtin_bit_cast(u16x2, w[0] & 0x7fff7fffu);
+    u16x2 m = __builtin_bit_cast(u16x2, w[0][0] & 0x7fff7fffu);
 #pragma unroll
-    for (int j = 1; j < 4; ++j) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[j] & 0x7fff7fffu));
+    for (uint32_t j = 0; j < W; ++j)
+#pragma unroll
+      for (int k = (j == 0 ? 1 : 0); k < 4; ++k) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[j][k] & 0x7fff7fffu));
     const uint16_t b = m[0] > m[1] ? m[0] : m[1];
     nonfinite = b >= kInf;
     if (b > kInf) return slow();
     if constexpr (std::is_same<T, _Float16>::value) return __float_as_uint(float(__builtin_bit_cast(_Float16, b)));
     else return uint32_t(b) << 16;
   } else {
-    uint32_t m = w[0] & 0x7fffffffu;
+    uint32_t m = w[0][0] & 0x7fffffffu;
 #pragma unroll
-    for (int j = 1; j < 4; ++j) m = max(m, w[j] & 0x7fffffffu);
+    for (uint32_t j = 0; j < W; ++j)
+#pragma unroll
+      for (int k = (j == 0 ? 1 : 0); k < 4; ++k) m = max(m, w[j][k] & 0x7fffffffu);
     nonfinite = m >= 0x7f800000u;
     if (m > 0x7f800000u) return slow();
     return m;
   }
 }
 
-// The codes of the N elements of a 16-byte word, quantize() bitwise.  With
-// r the hardware reciprocal of the scale (within one ulp of 1/scale),
-// r_lo = RN(r * (1 - 2^-21)) and r_hi = RN(r * (1 + 2^-21)), the products
-// x * r_lo and x * r_hi bracket the IEEE quotient RN(x / scale); fma(x, r, M)
-// with M = 1.5 * 2^23 rounds the exact product to the nearest integer n
-// (half to even) in the low mantissa bits, and rounding to the nearest
-// integer is monotone, so where both ends give the same n it is
-// rint(RN(x / scale)) -- every fp16 row maximum and source value, and random
-// fp32 rows, are checked by tests/cpp/quant_bracket_check.c.  Where the ends
-// differ (a quotient within ~2^-21 relative of a half-integer, e.g. an exact
-// tie), where the word holds a non-finite element, or where the reciprocal is
-// not finite (force), the word takes the division and the clamp of
-// quantize() (a NaN quotient gives -127).  The ends are compared by a sum of
-// absolute differences of their low 16 bits (the two n differ by at most 1).
-template <class T, uint32_t N>
-__device__ __forceinline__ void quantize_word(const u32x4& w, float scale, float r_lo, float r_hi, bool force,
-                                              uint32_t (&t)[N]) {
-  const T* e = reinterpret_cast<const T*>(&w);
-  uint32_t amb = force ? 1u : 0u;
+// The codes of a lane's W words of N elements of one row, quantize()
+// bitwise, with r the hardware reciprocal of the scale (within one ulp of
+// 1/scale) and M = 1.5 * 2^23 (RN(q + M) holds rint(q), half to even, in its
+// low mantissa bits).
+//  - fp16 / bf16 sources: the quotient as q0 = RN(x * r), residual
+//    fma(-q0, scale, x), q = fma(residual, r, q0) -- equal to the IEEE
+//    quotient RN(x / scale) for every fp16 and bf16 row maximum a with scale
+//    RN(a / 127) >= 2^-100, every such r and every source value |x| <= a
+//    (exhaustive: tests/cpp/quant_fmadiv_check.c), so no element needs a
+//    check.
+//  - fp32 sources: with r_lo = RN(r * (1 - 2^-21)) and r_hi = RN(r * (1 +
+//    2^-21)) the products x * r_lo and x * r_hi bracket RN(x / scale); fma(x,
+//    r, M) rounds the exact product to the nearest integer, and rounding to
+//    the nearest integer is monotone, so where both ends give the same
+//    integer it is rint(RN(x / scale)) (tests/cpp/quant_bracket_check.c).
+//    The ends are compared by sums of absolute differences of their low 16
+//    bits (the two integers differ by at most 1), in two chains; a lane where
+//    some pair differs (a quotient within ~2^-21 relative of a half-integer,
+//    e.g. an exact tie) divides.
+// A lane whose words hold a non-finite element, or whose row's reciprocal is
+// not finite or scale below 2^-100 (force), takes the division and the clamp
+// of quantize() (a NaN quotient gives -127).
+template <class T, uint32_t N, uint32_t W>
+__device__ __forceinline__ void quantize_lane(const u32x4 (&w)[W], float scale, float r_lo, float r_hi, bool force,
+                                              uint32_t (&t)[W * N]) {
+  uint32_t amb0 = force ? 1u : 0u, amb1 = 0u;
+  const float r = r_lo;  // fp16 / bf16: the reciprocal itself (recip_of)
 #pragma unroll
-  for (uint32_t i = 0; i < N; ++i) {
-    const float x = to_f32(e[i]);
-    const float lo = fmaf(x, r_lo, kRoundMagic);
-    const float hi = fmaf(x, r_hi, kRoundMagic);
-    amb = __builtin_amdgcn_sad_u16(__float_as_uint(lo), __float_as_uint(hi), amb);
-    t[i] = __float_as_uint(lo);
+  for (uint32_t j = 0; j < W; ++j) {
+    const T* e = reinterpret_cast<const T*>(&w[j]);
+#pragma unroll
+    for (uint32_t i = 0; i < N; ++i) {
+      const float x = to_f32(e[i]);
+      if constexpr (sizeof(T) == 2) {
+        // RN(x * r + 0): an fma (fp16 x read in place by the mixed-precision
+        // form); the +0 addend only turns a -0 product into +0, which gives
+        // the same code, and keeps the compiler from making it a multiply.
+        const float q0 = fmaf(x, r, 0.0f);
+        const float q = fmaf(fmaf(-q0, scale, x), r, q0);
+        t[N * j + i] = __float_as_uint(q + kRoundMagic);
+      } else {
+        const float lo = fmaf(x, r_lo, kRoundMagic);
+        const float hi = fmaf(x, r_hi, kRoundMagic);
+        if (i & 1u) amb1 = __builtin_amdgcn_sad_u16(__float_as_uint(lo), __float_as_uint(hi), amb1);
+        else amb0 = __builtin_amdgcn_sad_u16(__float_as_uint(lo), __float_as_uint(hi), amb0);
+        t[N * j + i] = __float_as_uint(lo);
+      }
+    }
   }
-  if (amb != 0u) {  // rare: one branch per word
+  if ((amb0 | amb1) != 0u) {  // rare: one branch per lane and row
 #pragma unroll
-    for (uint32_t i = 0; i < N; ++i)
-      t[i] = __float_as_uint(fminf(fmaxf(__builtin_rintf(to_f32(e[i]) / scale), -127.f), 127.f) + kRoundMagic);
+    for (uint32_t j = 0; j < W; ++j) {
+      const T* e = reinterpret_cast<const T*>(&w[j]);
+#pragma unroll
+      for (uint32_t i = 0; i < N; ++i)
+        t[N * j + i] = __float_as_uint(fminf(fmaxf(__builtin_rintf(to_f32(e[i]) / scale), -127.f), 127.f) + kRoundMagic);
+    }
   }
 }
 
-// The reciprocal bracket of quantize_word for one row's scale; force when the
-// reciprocal is not finite (a scale below the normal range).
-__device__ __forceinline__ void bracket_of(float scale, float& r_lo, float& r_hi, bool& force) {
+// The reciprocal terms of quantize_lane for one row's scale (fp16 / bf16: r
+// in r_lo; fp32: the bracket), and force where the reciprocal is not finite
+// or the scale is below 2^-100.
+template <class T>
+__device__ __forceinline__ void recip_of(float scale, float& r_lo, float& r_hi, bool& force) {
   const float r = __builtin_amdgcn_rcpf(scale);
-  r_lo = r * (1.0f - 0x1p-21f);
-  r_hi = r * (1.0f + 0x1p-21f);
-  force = !(r_hi <= 3.4028234663852886e38f);
+  if constexpr (sizeof(T) == 2) {
+    r_lo = r_hi = r;
+    force = !(r <= 3.4028234663852886e38f) || !(scale >= 0x1p-100f);
+  } else {
+    r_lo = r * (1.0f - 0x1p-21f);
+    r_hi = r * (1.0f + 0x1p-21f);
+    force = !(r_hi <= 3.4028234663852886e38f);
+  }
 }
 
 // Max over aligned groups of L lanes (L a power of two, 4..64), in every lane
@@ -331,13 +371,19 @@ __global__ __launch_bounds__(64 * kWaves) void append_tile_kernel(AppendArgs a) 
 
 // append_stream_kernel (prefill-sized appends from 16-byte aligned rows, dim
 // 64/128/256): one work-group of eight waves per (64 new tokens, kv head).
-// Wave w loads tokens 8w .. 8w + 7 row-major (LPR lanes per row, 16 bytes
-// each: one coalesced pass, every row read once), the row absmax is an xor
-// shuffle over those lanes, and K codes go out as each lane's contiguous
-// 16 / sizeof(T) bytes of the token's row.  V codes are transposed through
-// LDS ([dim][64 tokens], 68-byte rows) and stored 16 tokens per 16-byte store where those
-// 16 tokens fill 16 consecutive slots of one page starting on a 16-slot
-// boundary (a prefill chunk); any other group of 16 is stored byte by byte.
+// Wave w holds tokens 8w .. 8w + 7, eight lanes per token row: word j of a
+// lane is elements 16 / sizeof(T) * (8j + sub) .. of its row (sub = lane %
+// 8), so every load instruction reads whole 128-byte lines and every row is
+// read once.  The row absmax is a three-step DPP max over the eight lanes,
+// and the per-row work (scale, reciprocal) is shared by twice the elements
+// per lane of a sixteen-lane split (the same kernel with sixteen lanes per
+// row and a checked bracket rounding ran 6.62 us against 5.09 us at 4,096
+// fp16 tokens, its divisions at exact fp16 ties included).  K codes go out
+// as 8-byte (fp16 / bf16) or 4-byte pieces of each word.  V codes are
+// transposed through LDS ([dim][64 tokens], 68-byte rows) and stored 16
+// tokens per 16-byte store where those 16 tokens fill 16 consecutive slots
+// of one page starting on a 16-slot boundary (a prefill chunk); any other
+// group of 16 is stored byte by byte.
 // The pool stores are non-temporal (streaming): the codes are not read again
 // by this launch, and cached write-back stores measured slower (4,096 /
 // 16,384 / 65,536 tokens at d128: 8.2 / 23.2 / 86.8 us against 7.9 / 21.9 /
@@ -349,13 +395,15 @@ __global__ __launch_bounds__(64 * kWaves) void append_tile_kernel(AppendArgs a) 
 constexpr int kStreamWaves = 8;
 template <class T, int D, bool P2>  // P2: page_tokens is a power of two
 __global__ __launch_bounds__(64 * kStreamWaves) void append_stream_kernel(AppendArgs a) {
-  constexpr uint32_t EPL = 16 / sizeof(T);  // elements per lane per load
-  constexpr uint32_t LPR = D / EPL;         // lanes per row
-  static_assert(LPR >= 4 && LPR <= 64 && 64 % LPR == 0, "row split");
-  constexpr uint32_t RPL = 64 / LPR;        // rows per wave-load
-  // V codes [d][token] with 68-byte rows: a lane's eight code bytes go to
-  // eight dim rows, and the 16 lanes of a token row hit eight different LDS
-  // banks two by two (64-byte rows put all 16 on one bank).
+  constexpr uint32_t EPL = 16 / sizeof(T);  // elements per 16-byte word
+  constexpr uint32_t LPR = 8;               // lanes per row
+  constexpr uint32_t WPL = D / EPL / LPR;   // words per lane and row
+  static_assert(WPL >= 1 && D % (EPL * LPR) == 0, "row split");
+  constexpr uint32_t TPW = 64u / LPR;       // tokens per wave
+  static_assert(TPW * kStreamWaves == 64u, "64 tokens per work-group");
+  // V codes [d][token] with 68-byte rows: a lane's code bytes go to dim rows
+  // EPL apart, so the lanes of a token row hit different LDS banks (64-byte
+  // rows put them all on one bank).
   constexpr uint32_t VR = 68;
   __shared__ __attribute__((aligned(16))) uint8_t vt[D * VR];
   __shared__ uint32_t ids[64];
@@ -366,23 +414,25 @@ __global__ __launch_bounds__(64 * kStreamWaves) void append_stream_kernel(Append
   const uint32_t psh = __builtin_ctz(P);
   auto page_of = [&](uint32_t id) { return P2 ? id >> psh : id / P; };
   auto slot_of = [&](uint32_t id) { return P2 ? id & (P - 1u) : id % P; };
-  constexpr uint32_t TPW = 64u / kStreamWaves;  // tokens per wave
-  static_assert(TPW % RPL == 0, "a wave's tokens fill whole row slices");
-  constexpr uint32_t NI = TPW / RPL;  // row slices per lane
-  const uint32_t sub = lane % LPR, e0 = sub * EPL;
+  const uint32_t sub = lane % LPR, r = TPW * wave + lane / LPR;  // r: token of the tile
+  // Word j of a lane holds elements EPL * (LPR * j + sub) .. + EPL - 1 of its
+  // row, so each load instruction reads whole 128-byte lines of the rows.
+  auto elem0 = [&](uint32_t j) { return EPL * (LPR * j + sub); };
   // Every source load of the wave first (they do not depend on the slot
   // ids), so they are all in flight together; then the slot ids.
-  u32x4 wk[NI], wv[NI];
+  u32x4 wk[WPL], wv[WPL];
+  {
+    const uint32_t t = t0 + r;
 #pragma unroll
-  for (uint32_t i = 0; i < NI; ++i) {
-    const uint32_t t = t0 + TPW * wave + RPL * i + lane / LPR;
-    if (t < a.tokens) {
-      wk[i] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k_new) + size_t(t) * a.k_stride +
-                                              size_t(kv) * D + e0);
-      wv[i] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v_new) + size_t(t) * a.v_stride +
-                                              size_t(kv) * D + e0);
-    } else {
-      wk[i] = wv[i] = u32x4{0u, 0u, 0u, 0u};
+    for (uint32_t j = 0; j < WPL; ++j) {
+      if (t < a.tokens) {
+        wk[j] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k_new) + size_t(t) * a.k_stride +
+                                                size_t(kv) * D + elem0(j));
+        wv[j] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v_new) + size_t(t) * a.v_stride +
+                                                size_t(kv) * D + elem0(j));
+      } else {
+        wk[j] = wv[j] = u32x4{0u, 0u, 0u, 0u};
+      }
     }
   }
   if (wave == 0) {
@@ -395,34 +445,39 @@ __global__ __launch_bounds__(64 * kStreamWaves) void append_stream_kernel(Append
     if ((lane & 15u) == 0u) grp_ok[lane >> 4] = ((b >> (lane & ~15u)) & 0xffffull) == 0xffffull ? 1u : 0u;
   }
   __syncthreads();
-#pragma unroll
-  for (uint32_t i = 0; i < NI; ++i) {
-    const uint32_t r = TPW * wave + RPL * i + lane / LPR;  // token of the tile
+  {
     const uint32_t id = ids[r];
     bool knf, vnf;
-    const uint32_t ka = group_max_bits<LPR>(word_absmax_bits<T, EPL>(wk[i], knf));  // the row's lanes are an aligned group
-    const uint32_t va = group_max_bits<LPR>(word_absmax_bits<T, EPL>(wv[i], vnf));
+    const uint32_t ka = group_max_bits<LPR>(lane_absmax_bits<T, EPL, WPL>(wk, knf));  // the row's lanes are an aligned group
+    const uint32_t va = group_max_bits<LPR>(lane_absmax_bits<T, EPL, WPL>(wv, vnf));
     const float ks = scale_of(__uint_as_float(ka));
     const float vs = scale_of(__uint_as_float(va));
     float klo, khi, vlo, vhi;
     bool kf, vf;
-    bracket_of(ks, klo, khi, kf);
-    bracket_of(vs, vlo, vhi, vf);
-    uint32_t tk[EPL], tv[EPL];
-    quantize_word<T, EPL>(wk[i], ks, klo, khi, kf || knf, tk);
-    quantize_word<T, EPL>(wv[i], vs, vlo, vhi, vf || vnf, tv);
-    uint32_t kw[EPL / 4];
+    recip_of<T>(ks, klo, khi, kf);
+    recip_of<T>(vs, vlo, vhi, vf);
+    uint32_t tk[WPL * EPL], tv[WPL * EPL];
+    quantize_lane<T, EPL, WPL>(wk, ks, klo, khi, kf || knf, tk);
+    quantize_lane<T, EPL, WPL>(wv, vs, vlo, vhi, vf || vnf, tv);
 #pragma unroll
-    for (uint32_t e = 0; e < EPL / 4; ++e)  // low bytes of four words
-      kw[e] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(tk[4 * e + 3], tk[4 * e + 2], 0x0c0c0400u),
-                                    __builtin_amdgcn_perm(tk[4 * e + 1], tk[4 * e], 0x0c0c0400u), 0x05040100u);
+    for (uint32_t j = 0; j < WPL; ++j)
 #pragma unroll
-    for (uint32_t e = 0; e < EPL; ++e) vt[(e0 + e) * VR + r] = uint8_t(tv[e]);
+      for (uint32_t e = 0; e < EPL; ++e) vt[(elem0(j) + e) * VR + r] = uint8_t(tv[EPL * j + e]);
     if (id < cap) {
       const size_t row = (size_t(page_of(id)) * a.kv_heads + kv) * P + slot_of(id);
-      int8_t* const kdst = a.k + row * D + e0;
-      if constexpr (EPL == 8) __builtin_nontemporal_store(u32x2{kw[0], kw[1]}, reinterpret_cast<u32x2*>(kdst));
-      else __builtin_nontemporal_store(kw[0], reinterpret_cast<uint32_t*>(kdst));
+#pragma unroll
+      for (uint32_t j = 0; j < WPL; ++j) {
+        uint32_t kw[EPL / 4];
+#pragma unroll
+        for (uint32_t e = 0; e < EPL / 4; ++e) {  // low bytes of four codes
+          const uint32_t* const c = tk + EPL * j + 4 * e;
+          kw[e] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(c[3], c[2], 0x0c0c0400u),
+                                        __builtin_amdgcn_perm(c[1], c[0], 0x0c0c0400u), 0x05040100u);
+        }
+        int8_t* const kdst = a.k + row * D + elem0(j);
+        if constexpr (EPL == 8) __builtin_nontemporal_store(u32x2{kw[0], kw[1]}, reinterpret_cast<u32x2*>(kdst));
+        else __builtin_nontemporal_store(kw[0], reinterpret_cast<uint32_t*>(kdst));
+      }
       if (sub == 0) {
         __builtin_nontemporal_store(ks, a.k_scales + row);
         __builtin_nontemporal_store(vs, a.v_scales + row);

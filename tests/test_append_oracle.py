@@ -155,8 +155,32 @@ def test_fast_scale_division_is_the_ieee_quotient():
     assert np.any((a * c) != (a / np.float32(127)))
 
 
+def test_fma_quotient_is_the_ieee_quotient_for_16_bit_sources():
+    """For fp16 and bf16 sources the row-streaming append kernel takes the
+    quotient x / scale as q0 = RN(x * r), q = fma(fma(-q0, scale, x), r, q0)
+    with r the hardware reciprocal (append.hip quantize_lane), with no check.
+    tests/cpp/quant_fmadiv_check.c compares rint(q) with rint of the IEEE
+    quotient for every 3rd fp16 / 5th bf16 row maximum, every fp32 r within
+    one ulp of 1/scale and every source value below the maximum, both signs
+    (its stride-1 sweeps, 2.0e9 fp16 and 2.1e9 bf16 cases, also find no
+    mismatch).  Planted mistakes -- q0 without the residual step, and bf16
+    rows below the kernel's 2^-100 scale cutoff -- must be caught."""
+    import subprocess
+    from pathlib import Path
+    here = Path(__file__).resolve().parent / "cpp"
+    subprocess.run(["make", "-s", "-C", str(here), "quant_fmadiv_check"], check=True)
+    exe = str(here / "quant_fmadiv_check")
+    for fmt, stride in (("fp16", "3"), ("bf16", "5")):
+        r = subprocess.run([exe, fmt, stride], capture_output=True, text=True)
+        assert r.returncode == 0 and " 0 mismatches" in r.stdout, r.stdout
+    for fmt, mode in (("fp16", "1"), ("bf16", "2")):
+        bad = subprocess.run([exe, fmt, "3", mode], capture_output=True, text=True)
+        assert bad.returncode == 1 and " 0 mismatches" not in bad.stdout, (fmt, mode, bad.stdout)
+
+
 def test_bracketed_code_rounding_is_the_ieee_quotient():
-    """The row-streaming append kernel rounds x / scale to its code from two
+    """The row-streaming append kernel rounds x / scale to its code (fp32
+    sources) from two
     fmas, x * RN(r * (1 -+ 2^-21)) + 1.5 * 2^23 with r the hardware
     reciprocal, and divides only where the two disagree (append.hip
     quantize_word).  tests/cpp/quant_bracket_check.c checks that agreement
