@@ -215,6 +215,55 @@ def test_append_non_finite_sources_match_oracle_bitwise(gpu, case):
                               w.view(np.uint8) if w.dtype == np.int8 else w.view(np.uint32)), f"{name} differs"
 
 
+@pytest.mark.parametrize("src", [kvb.KVB_SRC_F16, kvb.KVB_SRC_BF16])
+def test_append_every_16_bit_row_maximum_matches_oracle_bitwise(gpu, src):
+    """Every positive finite fp16 (bf16) value as a row maximum, through the
+    row-streaming kernel, whose fp16 / bf16 codes come from an fma quotient
+    with the hardware reciprocal and no check (exact for every reciprocal
+    within one ulp: tests/cpp/quant_fmadiv_check.c): one token per maximum,
+    its other elements the maximum times (2j + 1) / 254 (quotients at or next
+    to the half-integers) and random fractions of it with either sign, codes
+    and scales bitwise the CPU quantizer's.  bf16 maxima reach scales below
+    2^-100, which divide."""
+    import torch
+
+    if src == kvb.KVB_SRC_F16:
+        vals = np.arange(1, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    else:
+        vals = (np.arange(1, 0x7F80, dtype=np.uint32) << 16).view(np.float32)
+    tokens, kvh, D, P = len(vals), 1, 128, 64
+    rng = np.random.default_rng(0x7C00 + src)
+    x = np.empty((tokens, D), np.float64)
+    x[:, 0] = vals
+    x[:, 1:64] = vals[:, None].astype(np.float64) * (2 * np.arange(63) + 1) / 254.0
+    x[:, 64:] = vals[:, None].astype(np.float64) * rng.uniform(-1, 1, (tokens, 64))
+    tdt = getattr(torch, SRC[src])
+    bufs = []
+    for sgn in (1.0, -1.0):                     # K rows as built, V rows negated
+        t = torch.from_numpy((sgn * x).astype(np.float32)).to(tdt)
+        assert torch.equal(t[:, 0].float().abs(), torch.from_numpy(vals))  # the maxima are exact
+        bufs.append(t)
+    kbuf, vbuf = bufs
+    assert (kbuf.float().abs().max(dim=1).values == kbuf[:, 0].float().abs()).all()
+    pages = -(-tokens // P) + 1
+    order = rng.permutation(pages).astype(np.uint32)
+    tk = np.arange(tokens, dtype=np.uint32)
+    slots = (order[tk // P] * P + tk % P).astype(np.uint32)
+    pool = random_pool(pages, kvh, P, D, seed=11)
+    kn = kbuf.float().numpy().reshape(tokens, kvh, D)
+    vn = vbuf.float().numpy().reshape(tokens, kvh, D)
+    want = O.append_int8(*pool, kn, vn, slots, P)
+    dev = [torch.from_numpy(np.ascontiguousarray(a)).to(gpu) for a in pool]
+    s = kvb.append_shape(tokens, kvh, D, P, pages, src)
+    log(f"append of every {SRC[src]} row maximum: tokens={tokens} dim={D} page={P}")
+    kvb.append_kv(s, kbuf.to(gpu), vbuf.to(gpu), torch.from_numpy(slots.view(np.int32)).to(gpu), *dev)
+    torch.cuda.synchronize()
+    for name, g, w in zip(("k", "v", "k_scales", "v_scales"), dev, want):
+        got = g.cpu().numpy()
+        assert np.array_equal(got.view(np.uint8) if got.dtype == np.int8 else got.view(np.uint32),
+                              w.view(np.uint8) if w.dtype == np.int8 else w.view(np.uint32)), f"{name} differs"
+
+
 def test_cache_written_by_append_decodes(gpu):
     """Prefill a cfg2-shaped (shorter) cache through three append calls; it
     equals the synthetic generator's cache bitwise and decodes to FP64."""
