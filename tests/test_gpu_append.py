@@ -40,6 +40,8 @@ CASES = [
     (260, 1, 256, 64, kvb.KVB_SRC_BF16, 0),
     (512, 8, 128, 64, kvb.KVB_SRC_BF16, 4096),   # rows inside a wider buffer
     (257, 2, 100, 16, kvb.KVB_SRC_F16, 3),       # stride not a 16-byte multiple: element path
+    (288, 2, 256, 64, kvb.KVB_SRC_F16, 0),       # row-streaming, dim 256, random slots
+    (320, 2, 128, 48, kvb.KVB_SRC_F32, 0),       # row-streaming, page size not a power of two
 ]
 
 
@@ -89,6 +91,8 @@ PREFILL_CASES = [
     (700, 4, 64, 16, kvb.KVB_SRC_BF16, 8, ()),        # groups straddle 16-slot boundaries: byte stores
     (520, 8, 128, 64, kvb.KVB_SRC_F16, 0, (100, 263)),  # padding inside two groups
     (300, 1, 64, 64, kvb.KVB_SRC_F32, 48, ()),        # starts mid-page, crosses pages
+    (600, 2, 256, 48, kvb.KVB_SRC_F16, 0, ()),        # page size not a power of two (division path)
+    (400, 3, 128, 80, kvb.KVB_SRC_BF16, 16, (5,)),    # same, mid-page start, a padding entry
 ]
 
 
