@@ -192,7 +192,8 @@ __device__ __forceinline__ void quantize_lane(const u32x4 (&w)[W], float scale, 
 
 // The reciprocal terms of quantize_lane for one row's scale (fp16 / bf16: r
 // in r_lo; fp32: the bracket), and force where the reciprocal is not finite
-// or the scale is below 2^-100.
+// or the scale is below 2^-100 (the range the CPU checks cover; subnormal
+// scales in particular never reach the hardware reciprocal's fast path).
 template <class T>
 __device__ __forceinline__ void recip_of(float scale, float& r_lo, float& r_hi, bool& force) {
   const float r = __builtin_amdgcn_rcpf(scale);
@@ -202,7 +203,7 @@ __device__ __forceinline__ void recip_of(float scale, float& r_lo, float& r_hi, 
   } else {
     r_lo = r * (1.0f - 0x1p-21f);
     r_hi = r * (1.0f + 0x1p-21f);
-    force = !(r_hi <= 3.4028234663852886e38f);
+    force = !(r_hi <= 3.4028234663852886e38f) || !(scale >= 0x1p-100f);
   }
 }
 

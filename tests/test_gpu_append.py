@@ -183,9 +183,9 @@ NON_FINITE_CASES = [
 def test_append_non_finite_sources_match_oracle_bitwise(gpu, case):
     """Rows holding NaN and +-infinity: every kernel follows the one rule of
     the oracle (NaN left out of the absmax, an infinite element makes the
-    scale infinite, a NaN quotient clamps to -127), bitwise.  One row of
-    subnormal magnitudes (fp32 and bf16 sources) has a scale below the
-    normal range, whose reciprocal the kernels do not use."""
+    scale infinite, a NaN quotient clamps to -127), bitwise.  Rows of tiny
+    magnitudes (fp32 and bf16 sources) have scales below 2^-100, one of them
+    below the normal range, where the row-streaming kernel divides."""
     import torch
 
     tokens, kvh, D, P, src = case
@@ -202,6 +202,9 @@ def test_append_non_finite_sources_match_oracle_bitwise(gpu, case):
         x[2, 0, 5] = np.inf                        # an infinite element: infinite scale
         x[3, 0, :] = np.nan                        # an all-NaN row: scale 1, codes -127
         x[4, 0, :] = rng.standard_normal(D, dtype=np.float32) * np.float32(1e-39)  # subnormal scale
+        if tokens > 6:
+            x[5, 0, :] = rng.standard_normal(D, dtype=np.float32) * np.float32(1e-33)  # scale ~2^-115
+            x[6, 0, :] = rng.standard_normal(D, dtype=np.float32) * np.float32(1e-36)  # scale near 2^-125
         bufs.append(torch.from_numpy(x.reshape(tokens, kvh * D)).to(tdt))
     kbuf, vbuf = bufs
     pool = random_pool(pages, kvh, P, D, seed=tokens)
