@@ -1,5 +1,5 @@
 /* Check of the append stream kernel's code rounding (kvbridge_amd/csrc/append.hip,
- * quantize_word).  The kernel wants c = rint(RN(x / s)) (IEEE single division,
+ * quantize_lane, fp32 sources).  The kernel wants c = rint(RN(x / s)) (IEEE single division,
  * round half to even) for a source element x and its row's scale s.  With r a
  * reciprocal of s within one ulp (the documented accuracy of v_rcp_f32),
  *   r_lo = RN(r * (1 - 2^-K)),  r_hi = RN(r * (1 + 2^-K)),  M = 1.5 * 2^23,

@@ -183,7 +183,7 @@ def test_bracketed_code_rounding_is_the_ieee_quotient():
     sources) from two
     fmas, x * RN(r * (1 -+ 2^-21)) + 1.5 * 2^23 with r the hardware
     reciprocal, and divides only where the two disagree (append.hip
-    quantize_word).  tests/cpp/quant_bracket_check.c checks that agreement
+    quantize_lane).  tests/cpp/quant_bracket_check.c checks that agreement
     implies rint(RN(x / scale)) for every fp32 r within one ulp of 1/scale,
     every 5th fp16 row maximum with every fp16 source value below it (both
     signs), and random fp32 rows including their exact ties (its full fp16
